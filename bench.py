@@ -1,0 +1,369 @@
+"""Benchmark of the fused layer kernels on one MI355X.
+
+One *step* is one pass of the prefill-scale hot path at 4 x 2048 tokens, the
+shapes of BASELINE.json configs 4 and 5:
+
+  4a add_rms_norm   residual/hidden [8192, 2560]            -> total, normed
+  4b prefill_qkv    packed qkv [8192, 6144], q/k norm + RoPE -> Q, K/V cache
+  5a silu_mul       gate_up [8192, 19456]                    -> [8192, 9728]
+  5b embedding      8192 ids into [151936, 2560]             -> [8192, 2560]
+
+``value`` is the step's algorithmic HBM bytes (each input read once, each
+output written once) divided by its wall time, inputs resident in HBM.  Each
+kernel cycles through enough buffer sets that its distinct footprint exceeds
+twice the 256 MB Infinity Cache, so repeated calls cannot be served from it.
+Per-kernel durations come from HIP events recorded around every launch on the
+stream the kernels run on.  Decode configs 1-3 are timed as HIP graphs of
+back-to-back launches (microseconds per call).  The CPU baseline is the C
+oracle (single thread) on the same step's shapes, timed on this host.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from collections import deque
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from starter_amd.kernels.decode_fused import add_rms_norm, silu_mul  # noqa: E402
+from starter_amd.kernels.embedding import embedding  # noqa: E402
+from starter_amd.kernels.prefill import prefill_qkv  # noqa: E402
+from starter_amd.kernels.qk_norm_rope import qk_norm_rope  # noqa: E402
+from starter_amd.kernels.rmsnorm import rms_norm  # noqa: E402
+from starter_amd.kernels.rotary import default_inv_freq, rope_tables  # noqa: E402
+
+METRIC = ("achieved HBM GB/s (% of MI355X peak) + µs/call per fused kernel, decode & prefill")
+PEAK_GBPS = 8000.0          # MI355X HBM3E, AMD specification
+INFINITY_CACHE = 256 << 20  # bytes
+H, I, V = 2560, 9728, 151936
+NQ, NK, D = 32, 8, 128
+B, T = 4, 2048
+TOKENS = B * T
+CAPACITY = T + 128
+BF16 = torch.bfloat16
+
+
+def bf16_bytes(*numels: int) -> int:
+    return 2 * sum(numels)
+
+
+# Algorithmic bytes per call (each input once, each output once, gains and tables).
+BYTES = {
+    "add_rms_norm": bf16_bytes(4 * TOKENS * H, H),
+    "prefill_qkv": bf16_bytes(2 * TOKENS * (NQ + 2 * NK) * D, 2 * D, 2 * T * D),
+    "silu_mul": bf16_bytes(3 * TOKENS * I),
+    "embedding": bf16_bytes(2 * TOKENS * H) + 8 * TOKENS,
+}
+ROWS = {"add_rms_norm": TOKENS, "prefill_qkv": TOKENS * (NQ + 2 * NK), "silu_mul": TOKENS,
+        "embedding": TOKENS}
+ROW_UNIT = {"add_rms_norm": "rows", "prefill_qkv": "head-rows", "silu_mul": "rows",
+            "embedding": "tokens"}
+
+
+def normal(shape, mean=0.0, std=1.0, g=None, device="cuda"):
+    t = torch.empty(shape, dtype=torch.float32, device=device)
+    t.normal_(mean, std, generator=g)
+    return t.to(BF16)
+
+
+def sets_for(footprint: int) -> int:
+    """Buffer sets needed so the rotation's footprint exceeds 2x the Infinity Cache."""
+    return max(2, -(-2 * INFINITY_CACHE // footprint) + 1)
+
+
+class Workload:
+    """Device buffers of the prefill step, several rotating sets per kernel."""
+
+    def __init__(self, device):
+        g = torch.Generator(device=device).manual_seed(0)
+        self.w = normal((H,), 1.0, 0.1, g)
+        self.qw, self.kw = normal((D,), 1.0, 0.1, g), normal((D,), 1.0, 0.1, g)
+        self.cos, self.sin = rope_tables(default_inv_freq(5_000_000, D), CAPACITY, device=device)
+        n = sets_for(BYTES["add_rms_norm"])
+        self.add = [(normal((TOKENS, H), g=g), normal((TOKENS, H), g=g)) for _ in range(n)]
+        n = sets_for(BYTES["prefill_qkv"])
+        self.qkv = [(normal((TOKENS, (NQ + 2 * NK) * D), g=g),
+                     torch.zeros((B, NK, CAPACITY, D), dtype=BF16, device=device),
+                     torch.zeros((B, NK, CAPACITY, D), dtype=BF16, device=device))
+                    for _ in range(n)]
+        n = sets_for(BYTES["silu_mul"])
+        self.gate_up = [normal((TOKENS, 2 * I), g=g) for _ in range(n)]
+        self.table = normal((V, H), 0.0, 0.02, g)
+        n = sets_for(BYTES["embedding"])
+        self.ids = [torch.randint(0, V, (TOKENS,), generator=g, device=device) for _ in range(n)]
+        self.sets = {"add_rms_norm": len(self.add), "prefill_qkv": len(self.qkv),
+                     "silu_mul": len(self.gate_up), "embedding": len(self.ids)}
+        # The wrappers allocate fresh outputs; keeping the last `sets` of them
+        # alive makes the caching allocator rotate output buffers too.
+        self.live = {name: deque(maxlen=n) for name, n in self.sets.items()}
+
+    def launch(self, name: str, k: int):
+        if name == "add_rms_norm":
+            r, h = self.add[k % len(self.add)]
+            out = add_rms_norm(r, h, self.w, 1e-6)
+        elif name == "prefill_qkv":
+            qkv, kc, vc = self.qkv[k % len(self.qkv)]
+            out = prefill_qkv(qkv, self.qw, self.kw, 1e-6, 1e-6, self.cos, self.sin, kc, vc, T)
+        elif name == "silu_mul":
+            out = silu_mul(self.gate_up[k % len(self.gate_up)])
+        else:
+            out = embedding(self.ids[k % len(self.ids)], self.table)
+        self.live[name].append(out)
+
+
+KERNELS = ("embedding", "add_rms_norm", "prefill_qkv", "silu_mul")
+
+
+def run_prefill_step(work: Workload, steps: int, warmup: int):
+    for k in range(warmup):
+        for name in KERNELS:
+            work.launch(name, k)
+    torch.cuda.synchronize()
+    events = {name: [] for name in KERNELS}
+    t0 = time.perf_counter()
+    for k in range(steps):
+        for name in KERNELS:
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            work.launch(name, k)
+            end.record()
+            events[name].append((start, end))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    durations = {name: [s.elapsed_time(e) * 1e3 for s, e in pairs] for name, pairs in events.items()}
+    return wall, durations
+
+
+def graph_time(fn, calls_per_replay: int, replays: int = 50) -> float:
+    """Microseconds per call of ``fn`` captured ``calls_per_replay`` times in one graph."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(calls_per_replay):
+            fn()
+    for _ in range(5):
+        graph.replay()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(replays):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        end.synchronize()
+        samples.append(start.elapsed_time(end) * 1e3 / calls_per_replay)
+    return statistics.median(samples)
+
+
+def decode_configs(device) -> dict:
+    g = torch.Generator(device=device).manual_seed(0)
+    out = {}
+    # Config 1: RMSNorm [8, 2560].
+    x, w = normal((8, H), g=g), normal((H,), 1.0, 0.1, g)
+    us = graph_time(lambda: rms_norm(x, w, 1e-6), 100)
+    out["config1_rms_norm_8x2560"] = {"us_per_call": us, "bytes": bf16_bytes(2 * 8 * H, H)}
+    # Config 2: add + RMSNorm [64, 2560] chained over 36 layers.
+    residual = normal((64, H), 0.0, 4.0, g)
+    hidden = normal((36, 64, H), g=g)
+    ws = normal((36, H), 1.0, 0.1, g)
+
+    def layers():
+        r = residual
+        for layer in range(36):
+            r, _ = add_rms_norm(r, hidden[layer], ws[layer], 1e-6)
+        return r
+
+    us = graph_time(layers, 1) / 36
+    out["config2_add_rms_norm_64x2560_x36"] = {"us_per_call": us,
+                                               "bytes": bf16_bytes(4 * 64 * H, H)}
+    # Config 3: QK-norm + RoPE, 32 sequences, per-sequence positions in [0, 32767].
+    q, k = normal((32, 32, 1, D), g=g), normal((32, 8, 1, D), g=g)
+    qw, kw = normal((D,), 1.0, 0.1, g), normal((D,), 1.0, 0.1, g)
+    positions = torch.randint(0, 32768, (32,), generator=g, device=device)
+    cos, sin = rope_tables(default_inv_freq(5_000_000, D), positions=positions)
+    cos, sin = cos.view(32, 1, D), sin.view(32, 1, D)
+    us = graph_time(lambda: qk_norm_rope(q, k, qw, kw, cos, sin, 1e-6, 1e-6), 100)
+    out["config3_qk_norm_rope_b32"] = {"us_per_call": us,
+                                       "bytes": bf16_bytes(2 * 32 * 40 * D, 2 * D, 2 * 32 * D)}
+    for entry in out.values():
+        entry["gbps"] = entry["bytes"] / (entry["us_per_call"] * 1e3)
+        entry["frac"] = entry["gbps"] / PEAK_GBPS
+        entry["under_5us"] = entry["us_per_call"] < 5.0
+    return out
+
+
+def copy_bandwidth(device) -> float:
+    """GB/s of a plain 1 GiB device-to-device copy (read + write counted)."""
+    src = torch.empty(1 << 29, dtype=BF16, device=device)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(10):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        dst.copy_(src)
+        end.record()
+        end.synchronize()
+        samples.append(2 * src.numel() * 2 / (start.elapsed_time(end) * 1e6))
+    del src, dst
+    return statistics.median(samples)
+
+
+def cpu_baseline(reps: int = 3) -> dict:
+    """The C oracle (one thread) on the step's shapes; median of ``reps`` after one warmup."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    rng = np.random.default_rng(0)
+
+    def draw(shape, mean=0.0, std=1.0):
+        return O.bf16_bits((rng.standard_normal(shape, dtype=np.float32) * std + mean))
+
+    w = draw((H,), 1.0, 0.1)
+    res, hid = draw((TOKENS, H)), draw((TOKENS, H))
+    qkv = draw((TOKENS, (NQ + 2 * NK) * D))
+    qw, kw = draw((D,), 1.0, 0.1), draw((D,), 1.0, 0.1)
+    cos, sin = O.rope_table(O.default_inv_freq(5_000_000, D), n_pos=CAPACITY)
+    cache = np.zeros((B, NK, CAPACITY, D), np.uint16)
+    gate_up = draw((TOKENS, 2 * I))
+    table = draw((V, H), 0.0, 0.02)
+    ids = rng.integers(0, V, TOKENS)
+
+    def step():
+        O.embedding(ids, table)
+        O.add_rms_norm(res, hid, w, 1e-6)
+        O.prefill_qkv(qkv, qw, kw, 1e-6, 1e-6, cos, sin, cache, cache, T)
+        O.silu_mul(gate_up)
+
+    step()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    seconds = statistics.median(times)
+    step_bytes = sum(BYTES.values())
+    return {"value": step_bytes / seconds / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"C oracle, whole 4x2048-token step (4 kernels), median of {reps} reps "
+                      f"after 1 warmup: {seconds * 1e3:.0f} ms/step",
+            "cpu": platform.processor() or platform.machine(), "host_cpus": os.cpu_count()}
+
+
+def pmc_traffic() -> dict | None:
+    """HBM bytes per silu_mul launch from the committed rocprofv3 PMC summary."""
+    path = ROOT / "profiles" / "silu_mul_prefill_pmc.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text())
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode configs")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the fused kernels are per-row and need no "
+              "collective; run with --gpus 1 (multi-GPU sharding is a design note only).",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    print(f"bench: device {torch.cuda.get_device_name(device)}", file=sys.stderr, flush=True)
+
+    with torch.inference_mode():
+        copy_gbps = copy_bandwidth(device)
+        print(f"bench: copy {copy_gbps:.0f} GB/s", file=sys.stderr, flush=True)
+        work = Workload(device)
+        torch.cuda.synchronize()
+        print(f"bench: buffer sets {work.sets}", file=sys.stderr, flush=True)
+        wall, durations = run_prefill_step(work, args.steps, args.warmup)
+        ms_per_step = wall * 1e3 / args.steps
+        step_bytes = sum(BYTES.values())
+        kernels = {}
+        for name in KERNELS:
+            d = durations[name]
+            mean_us, median_us = statistics.fmean(d), statistics.median(d)
+            kernels[name] = {
+                "us_per_call_median": median_us, "us_per_call_mean": mean_us,
+                "bytes_per_call": BYTES[name],
+                "gbps": BYTES[name] / (mean_us * 1e3),
+                "frac": BYTES[name] / (mean_us * 1e3) / PEAK_GBPS,
+                f"{ROW_UNIT[name]}_per_s": ROWS[name] / (median_us * 1e-6),
+                "buffer_sets": work.sets[name],
+            }
+            print(f"bench: {name:13s} {median_us:8.2f} us  {kernels[name]['gbps']:7.0f} GB/s "
+                  f"({100 * kernels[name]['frac']:.1f}% of peak)", file=sys.stderr, flush=True)
+        del work
+        torch.cuda.empty_cache()
+        decode = {} if args.no_decode else decode_configs(device)
+        for name, entry in decode.items():
+            print(f"bench: {name:34s} {entry['us_per_call']:6.2f} us/call", file=sys.stderr,
+                  flush=True)
+
+    dominant = max(KERNELS, key=lambda n: kernels[n]["us_per_call_mean"])
+    traffic = pmc_traffic()
+    roofline = {"kernel": dominant, "bound": "hbm", "achieved": kernels[dominant]["gbps"],
+                "peak": PEAK_GBPS, "unit": "GB/s", "frac": kernels[dominant]["frac"],
+                "traffic": traffic["bytes_per_launch"] if traffic and traffic.get("kernel") == dominant else None,
+                "algorithmic_bytes": BYTES[dominant]}
+    result = {
+        "metric": METRIC,
+        "value": step_bytes / (ms_per_step * 1e6),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "prefill hot path, 4 x 2048 tokens: embedding gather + "
+                               "residual-add RMSNorm + packed QK-norm/RoPE/KV-cache write + "
+                               "SiLU*up (BASELINE configs 4a, 4b, 5a, 5b)",
+                   "tokens": TOKENS, "hidden": H, "intermediate": I, "vocab": V,
+                   "heads": [NQ, NK, D], "step_bytes": step_bytes},
+        "frac_of_peak": step_bytes / (ms_per_step * 1e6) / PEAK_GBPS,
+        "roofline": roofline,
+        "kernels": kernels,
+        "decode": decode,
+        "copy_gbps": copy_gbps,
+    }
+    if not args.no_cpu:
+        print("bench: CPU baseline (C oracle) ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

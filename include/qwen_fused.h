@@ -1,0 +1,163 @@
+/*
+ * qwen_fused.h - C ABI of the MI355X (gfx950) fused layer kernels of the
+ * Qwen3-4B decode engine: residual-add + RMSNorm, per-head Q/K RMSNorm fused
+ * with NeoX rotary embedding (three layouts), SiLU(gate)*up, the token
+ * embedding gather and the rotary cos/sin table builder.
+ *
+ * Conventions shared by every entry point:
+ *   - Tensors are plain device pointers.  "bf16" buffers hold IEEE bfloat16
+ *     bit patterns (uint16_t); "f32" buffers hold IEEE binary32.
+ *   - Sizes and strides are in ELEMENTS, never bytes.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Work is
+ *     only enqueued: no entry point synchronises, allocates, frees or reads a
+ *     device value on the host, so every call may be captured into a HIP graph.
+ *   - Return value: 0 on success; a negative QF_E* code for an argument error
+ *     detected on the host before anything is launched; otherwise the positive
+ *     hipError_t reported for the launch.  qf_error_string() names a code.
+ *   - The library keeps no mutable global state; calls are reentrant.
+ *   - Inputs are read-only.  Outputs must not alias inputs.
+ *
+ * Each entry point cites the reference (jadenpxrk/starter) Python/Triton
+ * function whose semantics it replaces.
+ */
+#ifndef QWEN_FUSED_H
+#define QWEN_FUSED_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QF_OK 0
+#define QF_E_ARG (-1)     /* null pointer, negative size, bad stride */
+#define QF_E_SHAPE (-2)   /* unsupported shape (e.g. head width != 128) */
+#define QF_E_ALIGN (-3)   /* pointer alignment the selected path needs */
+
+/* Library version: major*10000 + minor*100 + patch. */
+int qf_version(void);
+
+/* Static text for a status code returned by any qf_* call. */
+const char* qf_error_string(int status);
+
+/*
+ * RMSNorm over the last dimension, rounding to bf16 BEFORE the gain multiply:
+ *   var = sum(float(x)^2) / cols;  n = bf16(float(x) * (1 / sqrt(var + eps)))
+ *   out = bf16(float(n) * float(weight))
+ * Replaces engine/kernels/rmsnorm.py:39-62 (rms_norm + _rms_norm_kernel:12-36).
+ * Row r of x starts at x + (r / inner) * outer_stride + (r % inner) * inner_stride
+ * (a two-level row walk, so transposed 3-D inputs need no copy); the last
+ * dimension is contiguous.  out is contiguous [rows, cols].
+ */
+int qf_rms_norm(const void* x, int64_t rows, int64_t cols, int64_t inner,
+                int64_t outer_stride, int64_t inner_stride,
+                const void* weight, float eps, void* out, void* stream);
+
+/*
+ * Residual add folded into the following RMSNorm:
+ *   branch = splits == 0 ? bf16 branch[r, c]
+ *                        : bf16(((0 + p[0][r,c]) + p[1][r,c]) + ...)  (f32 partials)
+ *   total  = bf16(float(residual) + float(branch))        (stored)
+ *   normed = RMSNorm(total) with the cast placement of qf_rms_norm.
+ * Replaces engine/kernels/decode_fused.py:140-158 (add_rms_norm +
+ * _add_rms_norm_kernel:19-44).  residual/branch/total/normed are contiguous
+ * [rows, cols]; f32 partials are contiguous [splits, rows, cols].
+ */
+int qf_add_rms_norm(const void* residual, const void* branch, int32_t splits,
+                    const void* weight, int64_t rows, int64_t cols, float eps,
+                    void* total, void* normed, void* stream);
+
+/*
+ * SiLU(gate) * up on a packed [rows, 2*cols] projection (gate = first half):
+ *   a = bf16(g / (1 + exp(-g)));  out = bf16(float(a) * float(up))
+ * Replaces engine/kernels/decode_fused.py:161-169 (silu_mul +
+ * _silu_mul_kernel:47-56).  out is contiguous [rows, cols].
+ */
+int qf_silu_mul(const void* gate_up, int64_t rows, int64_t cols, void* out,
+                void* stream);
+
+/*
+ * Per-head Q/K RMSNorm + NeoX rotate-half RoPE for one decode token
+ * (head width 128):
+ *   n = bf16(bf16(x * inv) * w);  rot = [-n[64:], n[:64]]
+ *   out = bf16(bf16(n * cos) + bf16(rot * sin))
+ * Replaces engine/kernels/qk_norm_rope.py:47-73 (qk_norm_rope +
+ * _qk_norm_rope_kernel:8-44).  Head h of sequence b of q starts at
+ * q + b*q_bstride + h*q_hstride (likewise k); cos/sin rows of sequence b
+ * start at cos + b*cs_bstride (0 = one row shared by the batch).
+ * out_q is contiguous [batch, nq, 128], out_k [batch, nk, 128].
+ */
+int qf_qk_norm_rope(const void* q, const void* k, int64_t batch, int32_t nq,
+                    int32_t nk, int64_t q_bstride, int64_t q_hstride,
+                    int64_t k_bstride, int64_t k_hstride,
+                    const void* q_weight, const void* k_weight,
+                    const void* cos, const void* sin, int64_t cs_bstride,
+                    float q_eps, float k_eps, void* out_q, void* out_k,
+                    void* stream);
+
+/*
+ * Packed decode Q/K/V: per-head norm + RoPE of the q and k heads of one
+ * packed [q | k | v] row per sequence, at the slot `*position` read on the
+ * device; K and V rows go straight into cache slot `position`.
+ * Replaces engine/kernels/decode_fused.py:172-210 (qkv_norm_rope_cache +
+ * _qkv_norm_rope_cache_kernel:59-118).
+ *   qkv: bf16 [batch, (nq + 2 nk) * 128] when splits == 0, else f32 split-K
+ *        partials [splits, batch, (nq + 2 nk) * 128], summed in order from 0
+ *        and rounded once to bf16.
+ *   cos, sin: bf16 [capacity, 128] tables; position: one int64 on the device.
+ *   q_out: bf16 [batch, nq, 128]; key_cache, value_cache: bf16
+ *        [batch, nk, capacity, 128], only slot `position` is written.
+ * A position outside [0, capacity) writes no cache row and fills q_out with
+ * bf16 NaN (0x7FC0) instead of reading or writing out of bounds.
+ */
+int qf_qkv_norm_rope_cache(const void* qkv, int32_t splits, int64_t batch,
+                           int32_t nq, int32_t nk, const void* q_weight,
+                           const void* k_weight, float q_eps, float k_eps,
+                           const void* cos, const void* sin,
+                           const int64_t* position, int64_t capacity,
+                           void* q_out, void* key_cache, void* value_cache,
+                           void* stream);
+
+/*
+ * Packed prefill Q/K/V for a fresh prompt of `length` tokens per sequence:
+ * token t of sequence b sits at slot t.  Same arithmetic as
+ * qf_qkv_norm_rope_cache.  Replaces engine/kernels/prefill.py:66-96
+ * (prefill_qkv + _prefill_qkv:19-63).
+ *   qkv: bf16 [batch*length, (nq + 2 nk) * 128]; cos/sin bf16 [capacity, 128]
+ *   q_out: bf16 [batch, length, nq, 128]
+ *   key_cache/value_cache: bf16 [batch, nk, capacity, 128], only slots
+ *   [0, length) are written.
+ */
+int qf_prefill_qkv(const void* qkv, int64_t batch, int64_t length, int32_t nq,
+                   int32_t nk, const void* q_weight, const void* k_weight,
+                   float q_eps, float k_eps, const void* cos, const void* sin,
+                   int64_t capacity, void* q_out, void* key_cache,
+                   void* value_cache, void* stream);
+
+/*
+ * Token embedding gather, bit-exact: out[i, :] = table[ids[i], :].
+ * Replaces the nn.Embedding call base.embed_tokens(ids) at
+ * engine/decode_step.py:38, engine/prefill.py:34, engine/decode.py:19.
+ * An id outside [0, vocab) yields a zero row (never an out-of-bounds read).
+ */
+int qf_embedding(const int64_t* ids, int64_t n_ids, const void* table,
+                 int64_t vocab, int64_t cols, void* out, void* stream);
+
+/*
+ * Rotary cos/sin tables (Qwen3 default RoPE):
+ *   ang[p, j] = inv_freq[j] * float(pos_p)  (one f32 product),  j < half
+ *   cos[p, j] = cos[p, j + half] = bf16(cos(ang)),  sin likewise.
+ * pos_p = positions[p] when positions != NULL, else start + p.
+ * Replaces the table build of engine/decode.py:52-59, which evaluates
+ * Qwen3RotaryEmbedding.forward (transformers models/qwen3/modeling_qwen3.py)
+ * for every cache slot.  cos/sin are contiguous bf16 [n_pos, 2*half].
+ */
+int qf_rope_table(const float* inv_freq, int32_t half, const int64_t* positions,
+                  int64_t start, int64_t n_pos, void* cos, void* sin,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN_FUSED_H */

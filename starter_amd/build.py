@@ -1,0 +1,85 @@
+"""Build ``starter_amd/kernels/libqwen_fused.so`` from ``starter_amd/csrc/*.hip``.
+
+Every source is compiled for gfx950 only, with:
+
+* ``-ffp-contract=off`` - no silent multiply-add fusion; the kernels round to
+  bf16 at exactly the points the reference does, and an FMA would change the
+  f32 value being rounded;
+* ``-Xclang -target-feature -Xclang -packed-fp32-ops`` - no packed-f32 VALU
+  instructions (the host pass warns that it does not know the feature; that
+  warning is harmless);
+* HIP's default correctly rounded f32 divide and sqrt.
+
+Run ``python -m starter_amd.build`` or call :func:`build`.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+ROOT = PACKAGE.parent
+CSRC = PACKAGE / "csrc"
+OBJ_DIR = PACKAGE / "_build"
+LIBRARY = PACKAGE / "kernels" / "libqwen_fused.so"
+SOURCES = ("rmsnorm.hip", "silu_mul.hip", "qk_norm_rope.hip", "embedding.hip")
+ARCH = "gfx950"
+
+COMPILE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-I", str(ROOT / "include"),
+]
+
+
+def hipcc() -> str:
+    path = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError(f"hipcc not found (looked for {path})")
+    return path
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # The host pass always warns about the device-only packed-fp32 feature.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source and link the shared library; return its path."""
+    cc = hipcc()
+    OBJ_DIR.mkdir(exist_ok=True)
+    jobs = []
+    for name in SOURCES:
+        obj = OBJ_DIR / (Path(name).stem + ".o")
+        jobs.append((obj, [cc, *COMPILE_FLAGS, "-c", str(CSRC / name), "-o", str(obj)]))
+    workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
+    with concurrent.futures.ThreadPoolExecutor(workers) as pool:
+        for fut in [pool.submit(_run, cmd, verbose) for _, cmd in jobs]:
+            fut.result()
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+          *[str(obj) for obj, _ in jobs]], verbose)
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

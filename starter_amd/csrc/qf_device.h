@@ -1,0 +1,131 @@
+// Device helpers shared by the gfx950 kernels: bf16 <-> f32 conversion on
+// packed dwords, wavefront-64 DPP reductions, and the host-side launch
+// plumbing (status codes, stream casts).
+//
+// Numerics: every kernel is compiled with -ffp-contract=off so that no
+// multiply/add pair is fused into an FMA behind the source's back, and with
+// HIP's default correctly rounded f32 divide and sqrt.  f32 -> bf16 uses the
+// gfx950 v_cvt_pk_bf16_f32 instruction (round to nearest even).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/qwen_fused.h"
+
+namespace qf {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // 4 waves per workgroup everywhere
+
+// ---- bf16 <-> f32 -----------------------------------------------------------
+
+// Low / high bf16 of a packed dword, widened exactly to f32.
+__device__ __forceinline__ float lo_f32(uint32_t d) { return __uint_as_float(d << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t d) { return __uint_as_float(d & 0xffff0000u); }
+
+// Two f32 -> one dword of two bf16 (lo first), round to nearest even.
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+__device__ __forceinline__ uint16_t to_bf16(float x) {
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+__device__ __forceinline__ float from_bf16(uint16_t h) {
+  return __uint_as_float((uint32_t)h << 16);
+}
+
+// 8 bf16 (one 16-byte vector) <-> 8 f32.
+__device__ __forceinline__ void unpack8(const uint4& u, float* f) {
+  f[0] = lo_f32(u.x); f[1] = hi_f32(u.x);
+  f[2] = lo_f32(u.y); f[3] = hi_f32(u.y);
+  f[4] = lo_f32(u.z); f[5] = hi_f32(u.z);
+  f[6] = lo_f32(u.w); f[7] = hi_f32(u.w);
+}
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  uint4 u;
+  u.x = pack2(f[0], f[1]);
+  u.y = pack2(f[2], f[3]);
+  u.z = pack2(f[4], f[5]);
+  u.w = pack2(f[6], f[7]);
+  return u;
+}
+// Round 8 f32 to bf16 and widen back: the value a bf16 tensor would hold.
+__device__ __forceinline__ void round8(float* f) {
+  uint4 u = pack8(f);
+  unpack8(u, f);
+}
+
+// ---- DPP / cross-lane -------------------------------------------------------
+
+// DPP control words (GFX9 encoding).
+constexpr int kQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+constexpr int kRowRor8 = 0x128;     // row_ror:8, lane i <- lane (i+8) mod 16
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+// All-reduce sums over aligned lane groups of 8/16/32/64.  Every lane of a
+// group ends with the same bits (each step adds a commutative pair).  All
+// lanes of the wave must be active.
+template <int LANES>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(LANES == 8 || LANES == 16 || LANES == 32 || LANES == 64, "group");
+  v += dpp_f32<kQuadXor1>(v);
+  v += dpp_f32<kQuadXor2>(v);
+  v += dpp_f32<kRowHalfMirror>(v);
+  if constexpr (LANES >= 16) v += dpp_f32<kRowMirror>(v);
+  if constexpr (LANES >= 32) v += __shfl_xor(v, 16);
+  if constexpr (LANES >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+// ---- integer helpers --------------------------------------------------------
+
+// Unsigned 32-bit division by a run-time constant d >= 1 via a multiply-high
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994): q = (umulhi(n, m) + n) >> s.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d;
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  f.s = s;
+  f.m = (uint32_t)((((1ull << s) - d) << 32) / d + 1);
+  return f;
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  uint64_t t = (uint64_t)__umulhi(n, f.m) + n;
+  return (uint32_t)(t >> f.s);
+}
+
+// ---- host-side plumbing -----------------------------------------------------
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Status of the launch just enqueued on this thread.
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? QF_OK : (int)e;
+}
+
+}  // namespace qf

@@ -1,0 +1,248 @@
+// RMSNorm and residual-add + RMSNorm for gfx950.
+//
+// Arithmetic (engine/kernels/rmsnorm.py:19-36, engine/kernels/decode_fused.py:26-44;
+// Qwen3RMSNorm.forward in transformers models/qwen3/modeling_qwen3.py):
+//   total  = bf16(float(residual) + float(branch))          (add variant only)
+//   var    = sum(float(t)^2) / cols                          (f32)
+//   n      = bf16(float(t) * (1 / sqrt(var + eps)))          (IEEE sqrt and divide)
+//   out    = bf16(float(n) * float(w))
+// Split-K branch: branch = bf16(((0 + p0) + p1) + ... ) in f32, in split order.
+//
+// Layout: a group of LPR lanes owns one row; lane i holds the 16-byte vectors
+// i, i+LPR, ..., so each wave-wide load instruction covers LPR*16 contiguous
+// bytes.  The row stays in registers between the reduction and the output, so
+// every input byte is read once and every output byte written once.  The sum
+// of squares is reduced with DPP inside 16-lane rows and ds_bpermute across
+// them; no LDS allocation and no barrier.
+#include "qf_device.h"
+
+namespace qf {
+namespace {
+
+struct RmsArgs {
+  const uint16_t* x;       // residual (add) or input rows (plain)
+  const void* branch;      // bf16 [rows, cols] or f32 [splits, rows, cols]
+  const uint16_t* w;
+  uint16_t* total;         // add variant only
+  uint16_t* out;
+  int64_t rows, cols;
+  int64_t inner, outer_stride, inner_stride;  // plain variant row walk
+  int64_t split_stride;    // rows * cols
+  int32_t splits;
+  int32_t nvec;            // cols / 8
+  float eps;
+};
+
+template <bool ADD>
+__device__ __forceinline__ const uint16_t* row_base(const RmsArgs& a, int64_t r) {
+  if constexpr (ADD) {
+    return a.x + r * a.cols;
+  } else {
+    return a.x + (r / a.inner) * a.outer_stride + (r % a.inner) * a.inner_stride;
+  }
+}
+
+// Vector path: cols % 8 == 0 and every pointer / row stride 16-byte aligned.
+template <int LPR, int VPL, bool ADD>
+__global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
+  constexpr int kRowsPerBlock = kBlock / LPR;
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / LPR;
+  const bool live = row < a.rows;
+  const int64_t r = live ? row : 0;
+
+  const uint4* xin = reinterpret_cast<const uint4*>(row_base<ADD>(a, r));
+  float t[VPL][8];
+  float ss = 0.0f;
+
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int v = lane + k * LPR;
+    const bool on = live && v < a.nvec;
+    uint4 xv = on ? xin[v] : make_uint4(0, 0, 0, 0);
+    unpack8(xv, t[k]);
+    if constexpr (ADD) {
+      float y[8];
+      if (a.splits == 0) {
+        const uint4* b = reinterpret_cast<const uint4*>(
+            static_cast<const uint16_t*>(a.branch) + r * a.cols);
+        uint4 bv = on ? b[v] : make_uint4(0, 0, 0, 0);
+        unpack8(bv, y);
+      } else {
+        // f32 partials: two 16-byte halves per 8 columns, summed in split order.
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = 0.0f;
+        const float* p = static_cast<const float*>(a.branch) + r * a.cols + (int64_t)v * 8;
+        for (int s = 0; s < a.splits; ++s) {
+          float4 p0 = on ? reinterpret_cast<const float4*>(p)[0] : make_float4(0, 0, 0, 0);
+          float4 p1 = on ? reinterpret_cast<const float4*>(p)[1] : make_float4(0, 0, 0, 0);
+          y[0] += p0.x; y[1] += p0.y; y[2] += p0.z; y[3] += p0.w;
+          y[4] += p1.x; y[5] += p1.y; y[6] += p1.z; y[7] += p1.w;
+          p += a.split_stride;
+        }
+        round8(y);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[k][j] += y[j];
+      uint4 tv = pack8(t[k]);
+      unpack8(tv, t[k]);
+      if (on) reinterpret_cast<uint4*>(a.total + row * a.cols)[v] = tv;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += t[k][j] * t[k][j];
+  }
+
+  ss = group_sum<LPR>(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+
+  const uint4* wv = reinterpret_cast<const uint4*>(a.w);
+  uint4* o = reinterpret_cast<uint4*>(a.out + r * a.cols);
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int v = lane + k * LPR;
+    const bool on = live && v < a.nvec;
+    float n[8], w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) n[j] = t[k][j] * inv;
+    round8(n);
+    unpack8(on ? wv[v] : make_uint4(0, 0, 0, 0), w);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) n[j] *= w[j];
+    if (on) o[v] = pack8(n);
+  }
+}
+
+// Element value entering the norm: x, or bf16(x + branch) for the add variant.
+template <bool ADD>
+__device__ __forceinline__ float scalar_value(const RmsArgs& a, const uint16_t* x, int64_t row,
+                                              int64_t c) {
+  float t = from_bf16(x[c]);
+  if constexpr (ADD) {
+    float y;
+    if (a.splits == 0) {
+      y = from_bf16(static_cast<const uint16_t*>(a.branch)[row * a.cols + c]);
+    } else {
+      const float* p = static_cast<const float*>(a.branch) + row * a.cols + c;
+      y = 0.0f;
+      for (int s = 0; s < a.splits; ++s) y += p[(int64_t)s * a.split_stride];
+      y = from_bf16(to_bf16(y));
+    }
+    t = from_bf16(to_bf16(t + y));
+  }
+  return t;
+}
+
+// Scalar path for any width / alignment: one wave per row, two passes over
+// the inputs (the second recomputes the element instead of reading back the
+// stored sum).  Only odd shapes take it.
+template <bool ADD>
+__global__ __launch_bounds__(kBlock) void rms_scalar_kernel(RmsArgs a) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t row = (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+  if (row >= a.rows) return;  // wave-uniform
+  const uint16_t* x = row_base<ADD>(a, row);
+  float ss = 0.0f;
+  for (int64_t c = lane; c < a.cols; c += kWave) {
+    const float t = scalar_value<ADD>(a, x, row, c);
+    if constexpr (ADD) a.total[row * a.cols + c] = to_bf16(t);
+    ss += t * t;
+  }
+  ss = group_sum<kWave>(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+  for (int64_t c = lane; c < a.cols; c += kWave) {
+    const float n = from_bf16(to_bf16(scalar_value<ADD>(a, x, row, c) * inv));
+    a.out[row * a.cols + c] = to_bf16(n * from_bf16(a.w[c]));
+  }
+}
+
+template <int LPR, int VPL, bool ADD>
+int launch_vec(const RmsArgs& a, hipStream_t s) {
+  const int64_t blocks = (a.rows + (kBlock / LPR) - 1) / (kBlock / LPR);
+  hipLaunchKernelGGL((rms_vec_kernel<LPR, VPL, ADD>), dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
+  return launch_status();
+}
+
+template <bool ADD>
+int dispatch(RmsArgs a, bool vec_ok, hipStream_t s) {
+  if (a.rows == 0) return QF_OK;
+  if (!vec_ok) {
+    const int64_t blocks = (a.rows + 3) / 4;
+    hipLaunchKernelGGL((rms_scalar_kernel<ADD>), dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
+    return launch_status();
+  }
+  a.nvec = (int32_t)(a.cols / 8);
+  const int nv = a.nvec;
+  if (nv <= 8) return launch_vec<8, 1, ADD>(a, s);
+  if (nv <= 16) return launch_vec<16, 1, ADD>(a, s);
+  if (nv <= 32) return launch_vec<32, 1, ADD>(a, s);
+  switch ((nv + 63) / 64) {
+    case 1: return launch_vec<64, 1, ADD>(a, s);
+    case 2: return launch_vec<64, 2, ADD>(a, s);
+    case 3: return launch_vec<64, 3, ADD>(a, s);
+    case 4: return launch_vec<64, 4, ADD>(a, s);
+    case 5: return launch_vec<64, 5, ADD>(a, s);
+    case 6: return launch_vec<64, 6, ADD>(a, s);
+    case 7: return launch_vec<64, 7, ADD>(a, s);
+    case 8: return launch_vec<64, 8, ADD>(a, s);
+    case 9: case 10: return launch_vec<64, 10, ADD>(a, s);
+    case 11: case 12: return launch_vec<64, 12, ADD>(a, s);
+    case 13: case 14: return launch_vec<64, 14, ADD>(a, s);
+    case 15: case 16: return launch_vec<64, 16, ADD>(a, s);
+    default: break;
+  }
+  // Wider than 8192 columns: the scalar path handles any width.
+  const int64_t blocks = (a.rows + 3) / 4;
+  hipLaunchKernelGGL((rms_scalar_kernel<ADD>), dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace qf
+
+using namespace qf;
+
+extern "C" int qf_rms_norm(const void* x, int64_t rows, int64_t cols, int64_t inner,
+                           int64_t outer_stride, int64_t inner_stride,
+                           const void* weight, float eps, void* out, void* stream) {
+  if (rows < 0 || cols <= 0 || inner <= 0) return QF_E_ARG;
+  if (rows == 0) return QF_OK;
+  if (!x || !weight || !out) return QF_E_ARG;
+  if (rows > (int64_t)UINT32_MAX * 4) return QF_E_SHAPE;
+  RmsArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(weight);
+  a.out = static_cast<uint16_t*>(out);
+  a.rows = rows;
+  a.cols = cols;
+  a.inner = inner;
+  a.outer_stride = outer_stride;
+  a.inner_stride = inner_stride;
+  a.eps = eps;
+  const bool vec_ok = cols % 8 == 0 && outer_stride % 8 == 0 && inner_stride % 8 == 0 &&
+                      aligned16(x) && aligned16(weight) && aligned16(out);
+  return dispatch<false>(a, vec_ok, as_stream(stream));
+}
+
+extern "C" int qf_add_rms_norm(const void* residual, const void* branch, int32_t splits,
+                               const void* weight, int64_t rows, int64_t cols, float eps,
+                               void* total, void* normed, void* stream) {
+  if (rows < 0 || cols <= 0 || splits < 0) return QF_E_ARG;
+  if (rows == 0) return QF_OK;
+  if (!residual || !branch || !weight || !total || !normed) return QF_E_ARG;
+  if (rows > (int64_t)UINT32_MAX * 4) return QF_E_SHAPE;
+  RmsArgs a{};
+  a.x = static_cast<const uint16_t*>(residual);
+  a.branch = branch;
+  a.splits = splits;
+  a.split_stride = rows * cols;
+  a.w = static_cast<const uint16_t*>(weight);
+  a.total = static_cast<uint16_t*>(total);
+  a.out = static_cast<uint16_t*>(normed);
+  a.rows = rows;
+  a.cols = cols;
+  a.inner = 1;
+  a.eps = eps;
+  const bool vec_ok = cols % 8 == 0 && aligned16(residual) && aligned16(branch) &&
+                      aligned16(weight) && aligned16(total) && aligned16(normed);
+  return dispatch<true>(a, vec_ok, as_stream(stream));
+}

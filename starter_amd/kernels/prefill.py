@@ -1,0 +1,45 @@
+"""Packed prefill Q/K head norm, RoPE, and full-prefix static-cache writes (gfx950 HIP).
+
+Drop-in for ``engine/kernels/prefill.py`` (jadenpxrk/starter): same
+signature, validation and outputs.  Q is [B,T,Hq,128]; K/V keep the
+[B,Hkv,C,128] cache storage and only slots [0, T) are written.  Inputs and
+the angle tables are read-only.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+HEAD = 128
+
+
+def prefill_qkv(qkv, qw, kw, qeps, keps, cos, sin, keys, values, length):
+    """Read packed BF16 [B*T,(Hq+2Hkv)*128]; overwrite only cache [:,:,:T].
+
+    Angles are the model-generated [C,128] tables already owned by DecodeState.
+    Return a fresh, contiguous BF16 Q [B,T,Hq,128]. All tensors share a device.
+    This is a full fresh prefill at position zero, not chunked prefill.
+    Mirrors engine/kernels/prefill.py:66-96.
+    """
+    if keys.ndim != 4 or values.shape != keys.shape:
+        raise ValueError("K/V must have matching [B,Hkv,C,D] shapes")
+    batch, nk, capacity, width = keys.shape
+    if (batch < 1 or nk < 1 or width != HEAD or not 1 <= length <= capacity
+            or qkv.ndim != 2 or qkv.shape[0] != batch * length):
+        raise ValueError("unsupported full-prefill dimensions")
+    nq = qkv.shape[1] // width - 2 * nk
+    if (nq < 1 or nq % nk or qkv.shape[1] != (nq + 2 * nk) * width
+            or tuple(qw.shape) != (width,) or kw.shape != qw.shape
+            or tuple(cos.shape) != (capacity, width) or sin.shape != cos.shape):
+        raise ValueError("packed QKV, gains, or rotary tables disagree")
+    tensors = (qkv, qw, kw, cos, sin, keys, values)
+    if (not qkv.is_cuda or any(t.device != qkv.device or t.dtype != torch.bfloat16
+                              or not t.is_contiguous() for t in tensors)):
+        raise ValueError("prefill requires contiguous BF16 tensors on one CUDA device")
+    q = torch.empty((batch, length, nq, width), device=qkv.device, dtype=qkv.dtype)
+    _lib.call("qf_prefill_qkv", qkv.data_ptr(), batch, int(length), nq, nk, qw.data_ptr(),
+              kw.data_ptr(), float(qeps), float(keps), cos.data_ptr(), sin.data_ptr(), capacity,
+              q.data_ptr(), keys.data_ptr(), values.data_ptr(), _lib.stream(qkv.device))
+    return q

@@ -1,0 +1,86 @@
+"""The C-ABI library loads on a machine without a GPU, exports every entry
+point ``include/qwen_fused.h`` declares, and rejects bad arguments on the
+host before anything is launched.  No kernel runs here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import torch  # noqa: F401  (the library must bind to torch's HIP runtime)
+
+from starter_amd.kernels import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "qwen_fused.h"
+
+
+def declared() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(qf_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_and_binding_agree():
+    names = declared()
+    assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
+    assert len(names) == 10
+
+
+def test_library_exports_every_symbol():
+    lib = _lib.lib()
+    for name in declared():
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+
+
+def test_single_hip_runtime_in_process():
+    _lib.lib()
+    maps = Path("/proc/self/maps").read_text().splitlines()
+    runtimes = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(runtimes) == 1, runtimes
+
+
+def test_version_and_error_strings():
+    lib = _lib.lib()
+    assert lib.qf_version() == 100
+    assert lib.qf_error_string(0) == b"success"
+    assert b"invalid argument" in lib.qf_error_string(-1)
+    assert b"shape" in lib.qf_error_string(-2)
+    assert b"aligned" in lib.qf_error_string(-3)
+    assert lib.qf_error_string(-99) == b"unknown status"
+
+
+def test_host_side_argument_errors_launch_nothing():
+    lib = _lib.lib()
+    bogus = 0x1000  # never dereferenced: every call below fails its host checks first
+    assert lib.qf_rms_norm(bogus, -1, 8, 1, 0, 8, bogus, 1e-6, bogus, None) == -1
+    assert lib.qf_rms_norm(bogus, 4, 0, 4, 0, 8, bogus, 1e-6, bogus, None) == -1
+    assert lib.qf_rms_norm(None, 4, 8, 4, 0, 8, bogus, 1e-6, bogus, None) == -1
+    assert lib.qf_add_rms_norm(bogus, bogus, -1, bogus, 4, 8, 1e-6, bogus, bogus, None) == -1
+    assert lib.qf_silu_mul(bogus, 4, 0, bogus, None) == -1
+    assert lib.qf_qk_norm_rope(bogus, bogus, 2, 0, 8, 0, 0, 0, 0, bogus, bogus, bogus, bogus, 0,
+                               1e-6, 1e-6, bogus, bogus, None) == -1
+    # misaligned rows are rejected, not read
+    assert lib.qf_qk_norm_rope(bogus + 2, bogus, 2, 32, 8, 4096, 128, 1024, 128, bogus, bogus,
+                               bogus, bogus, 0, 1e-6, 1e-6, bogus, bogus, None) == -3
+    assert lib.qf_qkv_norm_rope_cache(bogus, 0, 2, 32, 8, bogus, bogus, 1e-6, 1e-6, bogus, bogus,
+                                      bogus, 0, bogus, bogus, bogus, None) == -1
+    assert lib.qf_prefill_qkv(bogus, 1, 9, 32, 8, bogus, bogus, 1e-6, 1e-6, bogus, bogus, 8,
+                              bogus, bogus, bogus, None) == -2
+    assert lib.qf_embedding(bogus + 4, 3, bogus, 10, 8, bogus, None) == -3
+    assert lib.qf_rope_table(bogus, 0, None, 0, 4, bogus, bogus, None) == -1
+
+
+def test_empty_inputs_are_no_ops():
+    lib = _lib.lib()
+    # zero rows / ids / positions return success without touching a pointer or the GPU
+    assert lib.qf_rms_norm(None, 0, 8, 1, 0, 8, None, 1e-6, None, None) == 0
+    assert lib.qf_add_rms_norm(None, None, 0, None, 0, 8, 1e-6, None, None, None) == 0
+    assert lib.qf_silu_mul(None, 0, 8, None, None) == 0
+    assert lib.qf_qk_norm_rope(None, None, 0, 32, 8, 0, 0, 0, 0, None, None, None, None, 0,
+                               1e-6, 1e-6, None, None, None) == 0
+    assert lib.qf_qkv_norm_rope_cache(None, 0, 0, 32, 8, None, None, 1e-6, 1e-6, None, None,
+                                      None, 16, None, None, None, None) == 0
+    assert lib.qf_prefill_qkv(None, 0, 4, 32, 8, None, None, 1e-6, 1e-6, None, None, 8,
+                              None, None, None, None) == 0
+    assert lib.qf_embedding(None, 0, None, 10, 8, None, None) == 0
+    assert lib.qf_rope_table(None, 64, None, 0, 0, None, None, None) == 0

@@ -1,0 +1,456 @@
+"""GPU parity of every HIP kernel against the CPU oracle (MI355X only).
+
+The bar: the embedding gather and every copied row
+(V cache, bf16 residual sum) bit-exact; every other bf16 output within one
+bf16 ulp of the oracle and within atol/rtol 1e-2, with at least 99% of
+elements bit-identical.  Cases follow the reference tests
+(tests/test_rmsnorm.py, tests/test_qk_norm_rope.py, tests/test_decode_step.py,
+tests/test_prefill.py) plus the five BASELINE.json configurations at full
+size, ragged/odd shapes that take the scalar paths, empty inputs, NaN-poisoned
+caches and out-of-range guards.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch.nn import functional as F
+
+from conftest import O, assert_bf16_close, bits, gen, normal, tensor
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
+
+from starter_amd.kernels.decode_fused import add_rms_norm, qkv_norm_rope_cache, silu_mul  # noqa: E402
+from starter_amd.kernels.embedding import embedding  # noqa: E402
+from starter_amd.kernels.prefill import prefill_qkv  # noqa: E402
+from starter_amd.kernels.qk_norm_rope import qk_norm_rope  # noqa: E402
+from starter_amd.kernels.rmsnorm import rms_norm  # noqa: E402
+from starter_amd.kernels.rotary import default_inv_freq, rope_tables  # noqa: E402
+
+DEV = "cuda"
+THETA = 5_000_000
+INV_FREQ = default_inv_freq(THETA, 128)
+
+
+def dev(t: torch.Tensor) -> torch.Tensor:
+    return t.to(DEV)
+
+
+def oracle_tables(capacity: int):
+    c, s = O.rope_table(INV_FREQ.numpy(), n_pos=capacity)
+    return tensor(c), tensor(s)
+
+
+def native_norm(x, weight, eps):
+    """tests/test_decode_step.py:56-58 of the reference (torch on the device)."""
+    f = x.float()
+    return (f * torch.rsqrt(f.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * weight
+
+
+def rotate_half(x):
+    return torch.cat((-x[..., 64:], x[..., :64]), dim=-1)
+
+
+def apply_rope(q, k, cos, sin):
+    """apply_rotary_pos_emb of transformers (elementwise, no batched matmul)."""
+    cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
+    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+
+# ------------------------------------------------------------------ rms_norm
+
+@pytest.mark.parametrize("width", [128, 2560])
+def test_rms_norm_reference_matrix(width):
+    """tests/test_rmsnorm.py of the reference, against the oracle and native torch."""
+    g = gen(0)
+    w = normal((width,), 1.0, 0.1, g=g)
+    for batch, length in ((1, 1), (4, 1), (16, 1), (4, 2048), (16, 512)):
+        for noncontiguous in (False, True):
+            x = normal((batch, length, width), g=g)
+            xd = dev(x)
+            if noncontiguous:
+                x, xd = x.transpose(0, 1), xd.transpose(0, 1)
+            before = xd.clone()
+            out = rms_norm(xd, dev(w), 1e-6)
+            assert out.shape == x.shape and out.is_contiguous()
+            expected = O.rms_norm(bits(x.contiguous()), bits(w), 1e-6)
+            assert_bf16_close(out, expected, min_exact=0.99, what=f"{batch}x{length}x{width}")
+            torch.testing.assert_close(out, native_norm(xd, dev(w), 1e-6), rtol=8e-3, atol=1e-5)
+            assert torch.equal(xd, before)
+
+
+def test_rms_norm_config1(golden):
+    g = gen(0)
+    x = normal((8, 2560), g=g)
+    w = normal((2560,), 1.0, 0.1, g=g)
+    out = rms_norm(dev(x), dev(w), 1e-6)
+    assert_bf16_close(out, O.rms_norm(bits(x), bits(w), 1e-6), min_exact=0.99)
+    assert np.array_equal(bits(x), golden["config1_rms_norm"]["x"])
+    assert_bf16_close(out, golden["config1_rms_norm"]["out"], min_exact=0.99)
+
+
+@pytest.mark.parametrize("rows,cols", [(3, 48), (5, 100), (7, 1000), (2, 3000), (3, 4096),
+                                       (2, 6144), (2, 8192), (2, 8191), (0, 2560)])
+def test_rms_norm_ragged_widths(rows, cols):
+    g = gen(1)
+    x, w = normal((rows, cols), g=g), normal((cols,), 1.0, 0.1, g=g)
+    out = rms_norm(dev(x), dev(w), 1e-6)
+    assert_bf16_close(out, O.rms_norm(bits(x), bits(w), 1e-6), min_exact=0.99)
+
+
+def test_rms_norm_misaligned_view_and_known_answers():
+    g = gen(2)
+    base = normal((6, 2561), g=g)
+    x = base[:, 1:]  # 2-byte offset rows: scalar path
+    w = normal((2560,), 1.0, 0.1, g=g)
+    out = rms_norm(dev(base)[:, 1:], dev(w), 1e-6)
+    assert_bf16_close(out, O.rms_norm(bits(x.contiguous()), bits(w), 1e-6), min_exact=0.99)
+    for c in (1.0, 2.0, -4.0):
+        const = torch.full((3, 2560), c, dtype=torch.bfloat16, device=DEV)
+        got = rms_norm(const, dev(w), 0.0)
+        assert torch.equal(got, (torch.sign(torch.tensor(c)) * w).to(torch.bfloat16).to(DEV).expand(3, -1))
+    zeros = rms_norm(torch.zeros(2, 2560, dtype=torch.bfloat16, device=DEV), dev(w), 1e-6)
+    assert int(torch.count_nonzero(zeros)) == 0
+
+
+# -------------------------------------------------------------- add_rms_norm
+
+@pytest.mark.parametrize("rows,cols", [(1, 2560), (4, 2560), (16, 2560), (3, 256), (5, 128),
+                                       (3, 48), (2, 100)])
+def test_add_rms_norm_matches_oracle(rows, cols):
+    """tests/test_decode_step.py:227-247 of the reference."""
+    g = gen(11)
+    x, y = normal((rows, cols), g=g), normal((rows, cols), 0.0, 3.0, g=g)
+    w = normal((cols,), g=g)
+    xd, yd = dev(x), dev(y)
+    before = (xd.clone(), yd.clone())
+    total, normed = add_rms_norm(xd, yd, dev(w), 1e-6)
+    e_total, e_normed = O.add_rms_norm(bits(x), bits(y), bits(w), 1e-6)
+    assert np.array_equal(bits(total), e_total)
+    assert torch.equal(total, xd + yd)  # atol 0
+    assert_bf16_close(normed, e_normed, min_exact=0.99)
+    torch.testing.assert_close(normed, native_norm(xd + yd, dev(w), 1e-6), rtol=8e-3, atol=1e-5)
+    torch.testing.assert_close(normed, rms_norm(total, dev(w), 1e-6), rtol=4e-3, atol=0)
+    assert torch.equal(xd, before[0]) and torch.equal(yd, before[1])
+    with pytest.raises(ValueError):
+        add_rms_norm(xd.float(), yd.float(), dev(w).float(), 1e-6)
+    with pytest.raises(ValueError):
+        add_rms_norm(xd, yd[:, :64].contiguous(), dev(w), 1e-6)
+
+
+@pytest.mark.parametrize("splits,rows", [(1, 3), (4, 16), (8, 64), (8, 5)])
+def test_add_rms_norm_split_k_partials(splits, rows):
+    g = gen(12)
+    x = normal((rows, 2560), g=g)
+    partials = torch.randn((splits, rows, 2560), generator=g) * 0.5
+    w = normal((2560,), 1.0, 0.1, g=g)
+    total, normed = add_rms_norm(dev(x), dev(partials), dev(w), 1e-6)
+    e_total, e_normed = O.add_rms_norm(bits(x), partials.numpy(), bits(w), 1e-6)
+    assert np.array_equal(bits(total), e_total)
+    assert_bf16_close(normed, e_normed, min_exact=0.99)
+
+
+def test_add_rms_norm_config2_chain():
+    """36 layer calls on [64, 2560]: residual ~ N(0,4), hidden ~ N(0,1), w ~ N(1,0.1)."""
+    g = gen(0)
+    residual = normal((64, 2560), 0.0, 4.0, g=g)
+    hidden = normal((36, 64, 2560), g=g)
+    w = normal((36, 2560), 1.0, 0.1, g=g)
+    r_dev, h_dev, w_dev = dev(residual), dev(hidden), dev(w)
+    r_host = bits(residual)
+    outs = []
+    for layer in range(36):
+        r_dev, normed = add_rms_norm(r_dev, h_dev[layer], w_dev[layer], 1e-6)
+        outs.append(normed)
+    for layer in range(36):
+        r_host, e_normed = O.add_rms_norm(r_host, bits(hidden[layer]), bits(w[layer]), 1e-6)
+        assert_bf16_close(outs[layer], e_normed, min_exact=0.99, what=f"layer {layer}")
+    assert np.array_equal(bits(r_dev), r_host)
+
+
+def test_add_rms_norm_config4a_full_size():
+    g = gen(0)
+    hidden, residual = normal((8192, 2560), g=g), normal((8192, 2560), g=g)
+    w = normal((2560,), 1.0, 0.1, g=g)
+    total, normed = add_rms_norm(dev(residual), dev(hidden), dev(w), 1e-6)
+    e_total, e_normed = O.add_rms_norm(bits(residual), bits(hidden), bits(w), 1e-6)
+    assert np.array_equal(bits(total), e_total)
+    assert_bf16_close(normed, e_normed, min_exact=0.99)
+
+
+# ----------------------------------------------------------------- silu_mul
+
+@pytest.mark.parametrize("rows,cols", [(1, 9728), (4, 9728), (16, 9728), (3, 512), (2, 96),
+                                       (3, 100), (0, 64)])
+def test_silu_mul_matches_oracle(rows, cols):
+    """tests/test_decode_step.py:250-262 of the reference."""
+    g = gen(12)
+    gate_up = normal((rows, 2 * cols), 0.0, 4.0, g=g)
+    if rows:
+        gate_up[0, :8] = torch.tensor([-40.0, -12.0, -1.0, 0.0, 1.0, 12.0, 40.0, 88.0])
+    out = silu_mul(dev(gate_up))
+    assert tuple(out.shape) == (rows, cols)
+    assert bool(torch.isfinite(out).all())
+    assert_bf16_close(out, O.silu_mul(bits(gate_up)), min_exact=0.99)
+    gate, up = dev(gate_up).chunk(2, dim=-1)
+    torch.testing.assert_close(out, F.silu(gate) * up, rtol=1e-2, atol=1e-3)
+    if rows:
+        with pytest.raises(ValueError):
+            silu_mul(dev(gate_up)[:, :-1].contiguous())
+
+
+def test_silu_mul_config5a_full_size():
+    g = gen(0)
+    gate_up = normal((8192, 19456), g=g)
+    out = silu_mul(dev(gate_up))
+    assert_bf16_close(out, O.silu_mul(bits(gate_up)), min_exact=0.999)
+
+
+def test_silu_mul_misaligned_scalar_path():
+    g = gen(13)
+    base = normal((5, 2 * 512 + 1), 0.0, 4.0, g=g)
+    view = dev(base)[:, 1:]
+    out = silu_mul(view.contiguous()[:, :])  # aligned copy: vector path
+    shifted = torch.empty(5 * 1024 + 1, dtype=torch.bfloat16, device=DEV)[1:].view(5, 1024)
+    shifted.copy_(view)
+    out2 = silu_mul(shifted)  # 2-byte offset: scalar path
+    expected = O.silu_mul(bits(base[:, 1:].contiguous()))
+    assert np.array_equal(bits(out), bits(out2))
+    assert_bf16_close(out2, expected, min_exact=0.99)
+
+
+# ------------------------------------------------------------- qk_norm_rope
+
+def test_qk_norm_rope_reference_matrix():
+    """tests/test_qk_norm_rope.py:134-175 of the reference."""
+    g = gen(19)
+    cos_t, sin_t = oracle_tables(16384 + 16)
+    for batch in (1, 3, 4, 16):
+        for shared in (True, False):
+            for position in (0, 511, 2047, 16383):
+                for strided in (False, True):
+                    width = 256 if strided else 128
+                    q = normal((batch, 32, 1, width), g=g)
+                    k = normal((batch, 8, 1, width), g=g)
+                    if strided:
+                        q, k = q[..., ::2], k[..., ::2]
+                    qw, kw = normal((128,), g=g), normal((128,), g=g)
+                    rows = torch.full((1 if shared else batch,), position)
+                    if not shared:
+                        rows = rows + torch.arange(batch)
+                    c, s = cos_t[rows].view(-1, 1, 128), sin_t[rows].view(-1, 1, 128)
+                    qd, kd = dev(q), dev(k)
+                    before = [t.clone() for t in (qd, kd)]
+                    oq, ok = qk_norm_rope(qd, kd, dev(qw), dev(kw), dev(c), dev(s), 1e-6, 3e-6)
+                    eq, ek = O.qk_norm_rope(bits(q.contiguous())[:, :, 0],
+                                            bits(k.contiguous())[:, :, 0], bits(qw), bits(kw),
+                                            bits(c), bits(s), 1e-6, 3e-6)
+                    what = f"b{batch} shared{shared} p{position} strided{strided}"
+                    assert oq.is_contiguous() and ok.is_contiguous()
+                    assert_bf16_close(bits(oq)[:, :, 0], eq, min_exact=0.99, what=what)
+                    assert_bf16_close(bits(ok)[:, :, 0], ek, min_exact=0.99, what=what)
+                    nq_ref, nk_ref = apply_rope(native_norm(qd, dev(qw), 1e-6),
+                                                native_norm(kd, dev(kw), 3e-6), dev(c), dev(s))
+                    torch.testing.assert_close(oq, nq_ref, rtol=0.02, atol=0.02)
+                    torch.testing.assert_close(ok, nk_ref, rtol=0.02, atol=0.02)
+                    for t, old in zip((qd, kd), before):
+                        assert torch.equal(t, old)
+
+
+def test_qk_norm_rope_exact_rounding_and_zeros():
+    g = gen(20)
+    q = torch.ones(3, 32, 1, 128, dtype=torch.bfloat16)
+    k = torch.full((3, 8, 1, 128), 2.0, dtype=torch.bfloat16)
+    qw, kw = normal((128,), g=g), normal((128,), g=g)
+    cos_t, sin_t = oracle_tables(8200)
+    c, s = cos_t[8191:8194].view(3, 1, 128), sin_t[8191:8194].view(3, 1, 128)
+    oq, ok = qk_norm_rope(dev(q), dev(k), dev(qw), dev(kw), dev(c), dev(s), 0.0, 0.0)
+    eq, ek = apply_rope(dev(q) * dev(qw), (dev(k) / 2) * dev(kw), dev(c), dev(s))
+    assert torch.equal(oq, eq) and torch.equal(ok, ek)
+    zq, zk = qk_norm_rope(dev(q).zero_(), dev(k).zero_(), dev(qw), dev(kw), dev(c), dev(s),
+                          1e-6, 1e-6)
+    assert int(torch.count_nonzero(zq)) == 0 and int(torch.count_nonzero(zk)) == 0
+
+
+def test_qk_norm_rope_config3():
+    """q [32,1,32,128], k [32,1,8,128], positions uniform in [0, 32767], theta 5e6."""
+    g = gen(0)
+    q, k = normal((32, 1, 32, 128), g=g), normal((32, 1, 8, 128), g=g)
+    qw, kw = normal((128,), 1.0, 0.1, g=g), normal((128,), 1.0, 0.1, g=g)
+    positions = torch.randint(0, 32768, (32,), generator=g)
+    cos_d, sin_d = rope_tables(INV_FREQ, positions=dev(positions))
+    c, s = cos_d.view(32, 1, 128), sin_d.view(32, 1, 128)
+    # [B,1,H,D] and [B,H,1,D] share the memory order when T = 1
+    oq, ok = qk_norm_rope(dev(q).view(32, 32, 1, 128), dev(k).view(32, 8, 1, 128), dev(qw),
+                          dev(kw), c, s, 1e-6, 1e-6)
+    eq, ek = O.qk_norm_rope(bits(q)[:, 0], bits(k)[:, 0], bits(qw), bits(kw), bits(c), bits(s),
+                            1e-6, 1e-6)
+    assert_bf16_close(bits(oq)[:, :, 0], eq, min_exact=0.99)
+    assert_bf16_close(bits(ok)[:, :, 0], ek, min_exact=0.99)
+
+
+# ------------------------------------------------------- qkv_norm_rope_cache
+
+@pytest.mark.parametrize("batch,heads,kv,capacity", [(1, 32, 8, 544), (3, 32, 8, 640),
+                                                     (16, 32, 8, 640), (2, 4, 2, 129)])
+def test_qkv_norm_rope_cache_values_slots_and_untouched_capacity(batch, heads, kv, capacity):
+    """tests/test_decode_step.py:264-293 of the reference."""
+    g = gen(13)
+    cos, sin = oracle_tables(capacity)
+    for position in (0, capacity // 2, capacity - 1):
+        qkv = normal((batch, (heads + 2 * kv) * 128), g=g)
+        qw, kw = normal((128,), g=g), normal((128,), g=g)
+        keys = torch.full((batch, kv, capacity, 128), float("nan"), dtype=torch.bfloat16,
+                          device=DEV)
+        values = keys.clone()
+        qd = dev(qkv)
+        before = qd.clone()
+        q = qkv_norm_rope_cache(qd, dev(qw), dev(kw), 1e-6, 3e-6, dev(cos), dev(sin),
+                                torch.tensor([position], device=DEV), keys, values)
+        eq, ek, ev = O.qkv_norm_rope_cache(bits(qkv), bits(qw), bits(kw), 1e-6, 3e-6, bits(cos),
+                                           bits(sin), position, bits(keys), bits(values))
+        assert tuple(q.shape) == (batch, heads, 1, 128) and q.is_contiguous()
+        assert_bf16_close(q, eq, min_exact=0.99)
+        assert_bf16_close(bits(keys)[:, :, position], ek[:, :, position], min_exact=0.99)
+        assert np.array_equal(bits(values)[:, :, position], ev[:, :, position])
+        untouched = torch.arange(capacity, device=DEV) != position
+        assert bool(keys[:, :, untouched].isnan().all())
+        assert bool(values[:, :, untouched].isnan().all())
+        assert bool(torch.isfinite(q).all())
+        assert torch.equal(qd, before)
+
+
+def test_qkv_exact_rounding_at_absolute_position():
+    """tests/test_decode_step.py:296-324 of the reference: capacity 640, slot 613."""
+    g = gen(15)
+    capacity, position = 640, 613
+    cos, sin = oracle_tables(capacity)
+    qw, kw = normal((128,), g=g), normal((128,), g=g)
+    v_rows = normal((3, 8 * 128), g=g)
+    qkv = torch.cat((torch.ones(3, 32 * 128), torch.full((3, 8 * 128), 2.0), v_rows.float()),
+                    dim=-1).to(torch.bfloat16)
+    keys = torch.zeros(3, 8, capacity, 128, dtype=torch.bfloat16, device=DEV)
+    values = keys.clone()
+    q = qkv_norm_rope_cache(dev(qkv), dev(qw), dev(kw), 0.0, 0.0, dev(cos), dev(sin),
+                            torch.tensor([position], device=DEV), keys, values)
+    c, s = dev(cos[position]).view(1, 1, 128), dev(sin[position]).view(1, 1, 128)
+    ones_q = torch.ones(3, 32, 1, 128, dtype=torch.bfloat16, device=DEV)
+    ones_k = torch.ones(3, 8, 1, 128, dtype=torch.bfloat16, device=DEV)
+    ref_q, ref_k = apply_rope(ones_q * dev(qw), ones_k * dev(kw), c, s)
+    assert torch.equal(q, ref_q)
+    assert torch.equal(keys[:, :, position], ref_k[:, :, 0])
+    assert torch.equal(values[:, :, position], dev(v_rows).view(3, 8, 128))
+    others = torch.arange(capacity, device=DEV) != position
+    assert int(keys[:, :, others].count_nonzero()) == 0
+    assert int(values[:, :, others].count_nonzero()) == 0
+
+
+def test_qkv_split_k_partials_and_position_guard():
+    g = gen(16)
+    batch, capacity = 5, 64
+    partials = torch.randn((4, batch, 48 * 128), generator=g) * 0.5
+    qw, kw = normal((128,), g=g), normal((128,), g=g)
+    cos, sin = oracle_tables(capacity)
+    keys = torch.zeros(batch, 8, capacity, 128, dtype=torch.bfloat16, device=DEV)
+    values = keys.clone()
+    pos = torch.tensor([37], device=DEV)
+    q = qkv_norm_rope_cache(dev(partials), dev(qw), dev(kw), 1e-6, 1e-6, dev(cos), dev(sin), pos,
+                            keys, values)
+    eq, ek, ev = O.qkv_norm_rope_cache(partials.numpy(), bits(qw), bits(kw), 1e-6, 1e-6,
+                                       bits(cos), bits(sin), 37, bits(keys), bits(values))
+    assert_bf16_close(q, eq, min_exact=0.99)
+    assert_bf16_close(keys, ek, min_exact=0.99)
+    assert np.array_equal(bits(values), ev)
+    # Out-of-range positions (forced from the host) write nothing and give NaN Q.
+    for bad in (-1, capacity, 1 << 40):
+        k2, v2 = torch.zeros_like(keys), torch.zeros_like(values)
+        q2 = qkv_norm_rope_cache(dev(partials), dev(qw), dev(kw), 1e-6, 1e-6, dev(cos),
+                                 dev(sin), torch.tensor([bad], device=DEV), k2, v2)
+        assert bool(q2.isnan().all())
+        assert int(k2.count_nonzero()) == 0 and int(v2.count_nonzero()) == 0
+
+
+# ------------------------------------------------------------- prefill_qkv
+
+@pytest.mark.parametrize("b,t,c,nq,nk", [(1, 3, 11, 32, 8), (2, 33, 41, 32, 8),
+                                         (1, 129, 137, 32, 8), (3, 17, 33, 32, 8),
+                                         (2, 7, 13, 4, 2), (2, 5, 9, 12, 4), (1, 1, 3, 4, 2)])
+def test_prefill_qkv_matches_oracle(b, t, c, nq, nk):
+    """tests/test_prefill.py:504-522 of the reference."""
+    g = gen(51)
+    p = normal((b * t, (nq + 2 * nk) * 128), g=g)
+    qw, kw = normal((128,), g=g), normal((128,), g=g)
+    cos, sin = oracle_tables(c)
+    k = torch.full((b, nk, c, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    v = k.clone()
+    pd = dev(p)
+    before = pd.clone()
+    q = prefill_qkv(pd, dev(qw), dev(kw), 1e-6, 3e-6, dev(cos), dev(sin), k, v, t)
+    eq, ek, ev = O.prefill_qkv(bits(p), bits(qw), bits(kw), 1e-6, 3e-6, bits(cos), bits(sin),
+                               bits(k), bits(v), t)
+    assert tuple(q.shape) == (b, t, nq, 128)
+    assert_bf16_close(q, eq, min_exact=0.99)
+    assert_bf16_close(bits(k)[:, :, :t], ek[:, :, :t], min_exact=0.99)
+    assert np.array_equal(bits(v)[:, :, :t], ev[:, :, :t])
+    assert bool(torch.isnan(k[:, :, t:]).all() & torch.isnan(v[:, :, t:]).all())
+    assert torch.equal(pd, before)
+
+
+def test_prefill_qkv_config4b_full_size():
+    """Prefill 4 x 2048 tokens: q [4,2048,32,128], k/v [4,8,C,128], slots 0..2047."""
+    g = gen(0)
+    b, t, capacity = 4, 2048, 2048 + 128
+    p = normal((b * t, 48 * 128), g=g)
+    qw, kw = normal((128,), 1.0, 0.1, g=g), normal((128,), 1.0, 0.1, g=g)
+    cos, sin = oracle_tables(capacity)
+    k = torch.zeros((b, 8, capacity, 128), dtype=torch.bfloat16, device=DEV)
+    v = torch.zeros_like(k)
+    q = prefill_qkv(dev(p), dev(qw), dev(kw), 1e-6, 1e-6, dev(cos), dev(sin), k, v, t)
+    eq, ek, ev = O.prefill_qkv(bits(p), bits(qw), bits(kw), 1e-6, 1e-6, bits(cos), bits(sin),
+                               bits(k), bits(v), t)
+    assert_bf16_close(q, eq, min_exact=0.99)
+    assert_bf16_close(k, ek, min_exact=0.99)
+    assert np.array_equal(bits(v), ev)
+
+
+# --------------------------------------------------------------- embedding
+
+def test_embedding_bit_exact_and_guards():
+    g = gen(3)
+    table = normal((1000, 2560), 0.0, 0.02, g=g)
+    td = dev(table)
+    ids = torch.randint(0, 1000, (4, 33), generator=g)
+    out = embedding(dev(ids), td)
+    assert tuple(out.shape) == (4, 33, 2560)
+    assert torch.equal(out, F.embedding(dev(ids), td))
+    assert np.array_equal(bits(out), O.embedding(ids.numpy(), bits(table)))
+    bad = embedding(torch.tensor([-1, 1000, 7, 1 << 40], device=DEV), td)
+    assert int(bad[[0, 1, 3]].count_nonzero()) == 0 and torch.equal(bad[2], td[7])
+    assert embedding(torch.empty(0, dtype=torch.int64, device=DEV), td).shape == (0, 2560)
+    # odd width: scalar path
+    odd = normal((50, 36), g=g)
+    ids2 = torch.randint(0, 50, (17,), generator=g)
+    assert torch.equal(embedding(dev(ids2), dev(odd)), F.embedding(dev(ids2), dev(odd)))
+
+
+def test_embedding_config5b_full_size():
+    g = gen(0)
+    table = normal((151936, 2560), 0.0, 0.02, g=g)
+    ids = torch.randint(0, 151936, (8192,), generator=g)
+    out = embedding(dev(ids), dev(table))
+    assert np.array_equal(bits(out), O.embedding(ids.numpy(), bits(table)))
+
+
+# ------------------------------------------------------------ rotary tables
+
+def test_rope_tables_match_oracle():
+    cos, sin = rope_tables(INV_FREQ, 32768, device=DEV)
+    ec, es = O.rope_table(INV_FREQ.numpy(), n_pos=32768)
+    assert_bf16_close(cos, ec, min_exact=0.999)
+    assert_bf16_close(sin, es, min_exact=0.999)
+    assert bool((cos[0] == 1).all()) and bool((sin[0] == 0).all())
+    pos = torch.tensor([5, 0, 32767, 2047], device=DEV)
+    pc, ps = rope_tables(INV_FREQ, positions=pos)
+    assert torch.equal(pc, cos[pos]) and torch.equal(ps, sin[pos])
