@@ -12,9 +12,11 @@ shapes of BASELINE.json configs 4 and 5:
 output written once) divided by its wall time, inputs resident in HBM.  Each
 kernel cycles through enough buffer sets that its distinct footprint exceeds
 twice the 256 MB Infinity Cache, so repeated calls cannot be served from it.
-Per-kernel durations come from HIP events recorded around every launch on the
-stream the kernels run on.  Decode configs 1-3 are timed as HIP graphs of
-back-to-back launches (microseconds per call).  The CPU baseline is the C
+The step is replayed from captured HIP graphs (as the engine replays its
+captured prefill), so host launch overhead is not part of the GPU timeline.
+Per-kernel durations come from HIP events around graphs of 24 back-to-back
+launches of one kernel (rotating its buffer sets), divided by 24.  Decode
+configs 1-3 are timed the same way (microseconds per call).  The CPU baseline is the C
 oracle (single thread) on the same step's shapes, timed on this host.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
@@ -124,43 +126,26 @@ class Workload:
 
 
 KERNELS = ("embedding", "add_rms_norm", "prefill_qkv", "silu_mul")
+STEPS_PER_GRAPH = 8  # one captured graph holds this many consecutive steps
 
 
-def run_prefill_step(work: Workload, steps: int, warmup: int):
-    for k in range(warmup):
-        for name in KERNELS:
-            work.launch(name, k)
-    torch.cuda.synchronize()
-    events = {name: [] for name in KERNELS}
-    t0 = time.perf_counter()
-    for k in range(steps):
-        for name in KERNELS:
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record()
-            work.launch(name, k)
-            end.record()
-            events[name].append((start, end))
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    durations = {name: [s.elapsed_time(e) * 1e3 for s, e in pairs] for name, pairs in events.items()}
-    return wall, durations
-
-
-def graph_time(fn, calls_per_replay: int, replays: int = 50) -> float:
-    """Microseconds per call of ``fn`` captured ``calls_per_replay`` times in one graph."""
+def capture(fn):
+    """Capture ``fn``'s launches into a HIP graph (after warmups on the capture stream)."""
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        for _ in range(3):
+        for _ in range(2):
             fn()
     torch.cuda.current_stream().wait_stream(stream)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        for _ in range(calls_per_replay):
-            fn()
-    for _ in range(5):
-        graph.replay()
+        fn()
     torch.cuda.synchronize()
+    return graph
+
+
+def timed_replays(graph, replays: int) -> list[float]:
+    """Microseconds of each replay, from HIP events on the replay stream."""
     samples = []
     for _ in range(replays):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -168,8 +153,60 @@ def graph_time(fn, calls_per_replay: int, replays: int = 50) -> float:
         graph.replay()
         end.record()
         end.synchronize()
-        samples.append(start.elapsed_time(end) * 1e3 / calls_per_replay)
-    return statistics.median(samples)
+        samples.append(start.elapsed_time(end) * 1e3)
+    return samples
+
+
+def kernel_durations(work: Workload, calls: int, replays: int) -> dict:
+    """Per-kernel microseconds per call: a graph of ``calls`` back-to-back
+    launches of one kernel, rotating its buffer sets, replayed ``replays``
+    times.  Returns every replay's per-call average."""
+    out = {}
+    for name in KERNELS:
+        graph = capture(lambda: [work.launch(name, k) for k in range(calls)])
+        graph.replay()
+        torch.cuda.synchronize()
+        out[name] = [t / calls for t in timed_replays(graph, replays)]
+        del graph
+    return out
+
+
+def run_prefill_step(work: Workload, steps: int, warmup: int):
+    """Wall time of exactly ``steps`` steps, replayed from graphs of
+    STEPS_PER_GRAPH consecutive steps (plus one graph for the remainder)."""
+    def steps_fn(first, count):
+        def fn():
+            for k in range(first, first + count):
+                for name in KERNELS:
+                    work.launch(name, k)
+        return fn
+
+    full, rest = divmod(steps, STEPS_PER_GRAPH)
+    graph = capture(steps_fn(0, STEPS_PER_GRAPH))
+    tail = capture(steps_fn(0, rest)) if rest else None
+    for _ in range(max(1, -(-warmup // STEPS_PER_GRAPH))):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(full):
+        graph.replay()
+    if tail is not None:
+        tail.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, start.elapsed_time(end) * 1e-3
+
+
+def graph_time(fn, calls_per_replay: int, replays: int = 50) -> float:
+    """Median microseconds per call of ``fn`` captured ``calls_per_replay`` times in one graph."""
+    graph = capture(lambda: [fn() for _ in range(calls_per_replay)])
+    for _ in range(5):
+        graph.replay()
+    torch.cuda.synchronize()
+    return statistics.median(t / calls_per_replay for t in timed_replays(graph, replays))
 
 
 def decode_configs(device) -> dict:
@@ -304,7 +341,8 @@ def main() -> int:
         work = Workload(device)
         torch.cuda.synchronize()
         print(f"bench: buffer sets {work.sets}", file=sys.stderr, flush=True)
-        wall, durations = run_prefill_step(work, args.steps, args.warmup)
+        durations = kernel_durations(work, calls=24, replays=max(5, args.steps // 24))
+        wall, gpu_seconds = run_prefill_step(work, args.steps, args.warmup)
         ms_per_step = wall * 1e3 / args.steps
         step_bytes = sum(BYTES.values())
         kernels = {}
@@ -316,11 +354,13 @@ def main() -> int:
                 "bytes_per_call": BYTES[name],
                 "gbps": BYTES[name] / (mean_us * 1e3),
                 "frac": BYTES[name] / (mean_us * 1e3) / PEAK_GBPS,
-                f"{ROW_UNIT[name]}_per_s": ROWS[name] / (median_us * 1e-6),
+                f"{ROW_UNIT[name]}_per_s": ROWS[name] / (mean_us * 1e-6),
                 "buffer_sets": work.sets[name],
             }
-            print(f"bench: {name:13s} {median_us:8.2f} us  {kernels[name]['gbps']:7.0f} GB/s "
+            print(f"bench: {name:13s} {mean_us:8.2f} us  {kernels[name]['gbps']:7.0f} GB/s "
                   f"({100 * kernels[name]['frac']:.1f}% of peak)", file=sys.stderr, flush=True)
+        print(f"bench: step {ms_per_step * 1e3:.1f} us wall, {gpu_seconds * 1e6 / args.steps:.1f} us "
+              f"GPU", file=sys.stderr, flush=True)
         del work
         torch.cuda.empty_cache()
         decode = {} if args.no_decode else decode_configs(device)

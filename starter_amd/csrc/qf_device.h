@@ -71,27 +71,43 @@ constexpr int kRowMirror = 0x140;
 constexpr int kRowRor8 = 0x128;     // row_ror:8, lane i <- lane (i+8) mod 16
 
 template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
 }
 
-// All-reduce sums over aligned lane groups of 8/16/32/64.  Every lane of a
-// group ends with the same bits (each step adds a commutative pair).  All
-// lanes of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __double_as_longlong(v);
+  const uint32_t lo = dpp_u32<CTRL>((uint32_t)u);
+  const uint32_t hi = dpp_u32<CTRL>((uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// All-reduce sum over aligned lane groups of 8/16/32/64 lanes, in f64.  Every
+// lane of a group ends with the same bits (each step adds a commutative pair);
+// all lanes of the wave must be active.  The RMSNorm kernels feed it exact f32 squares of
+// bf16 values (at most 16 significant bits each), so for any realistic row the
+// f64 partial sums are exact and the result does not depend on the reduction
+// order: rounding it once to f32 gives the correctly rounded f32 sum of
+// squares, bit-identical to any other exact evaluation.
 template <int LANES>
-__device__ __forceinline__ float group_sum(float v) {
+__device__ __forceinline__ double group_sum_f64(double v) {
   static_assert(LANES == 8 || LANES == 16 || LANES == 32 || LANES == 64, "group");
-  v += dpp_f32<kQuadXor1>(v);
-  v += dpp_f32<kQuadXor2>(v);
-  v += dpp_f32<kRowHalfMirror>(v);
-  if constexpr (LANES >= 16) v += dpp_f32<kRowMirror>(v);
+  v += dpp_f64<kQuadXor1>(v);
+  v += dpp_f64<kQuadXor2>(v);
+  v += dpp_f64<kRowHalfMirror>(v);
+  if constexpr (LANES >= 16) v += dpp_f64<kRowMirror>(v);
   if constexpr (LANES >= 32) v += __shfl_xor(v, 16);
   if constexpr (LANES >= 64) v += __shfl_xor(v, 32);
   return v;
+}
+
+// 1 / sqrt(mean + eps) from an exact f64 sum of squares over n elements, with
+// every f32 step correctly rounded (IEEE divide and sqrt):
+//   var = f32(sum) / n;  inv = 1 / sqrt(var + eps).
+__device__ __forceinline__ float inv_rms(double sum_sq, float n, float eps) {
+  const float var = (float)sum_sq / n;
+  return 1.0f / sqrtf(var + eps);
 }
 
 // ---- integer helpers --------------------------------------------------------

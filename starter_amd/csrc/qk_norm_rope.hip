@@ -10,7 +10,7 @@
 //                           written to cache slots [0, T) (engine/kernels/prefill.py:19-63)
 //
 // Arithmetic per head row x[0..127] (same cast chain in every layout):
-//   inv = 1 / sqrt(sum(x^2) / 128 + eps)
+//   inv = 1 / sqrt(f32(sum(x^2)) / 128 + eps)   (sum exact in f64, rounded once)
 //   n   = bf16(bf16(x * inv) * w)
 //   rot = [-n[64:], n[:64]]
 //   out = bf16(bf16(n * cos) + bf16(rot * sin))
@@ -44,11 +44,10 @@ __device__ __forceinline__ uint4 select4(bool c, const uint4& a, const uint4& b)
 // representable in bf16).  Returns the 8 bf16 outputs of this lane.
 __device__ __forceinline__ uint4 norm_rope(const float* x, uint4 wv, uint4 cv, uint4 sv,
                                            float eps, int l16) {
-  float ss = 0.0f;
+  double ss = 0.0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
-  ss = group_sum<kLanes>(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)kD + eps);
+  for (int j = 0; j < 8; ++j) ss += (double)(x[j] * x[j]);  // exact squares, exact sum
+  const float inv = inv_rms(group_sum_f64<kLanes>(ss), (float)kD, eps);
 
   float n[8], w[8];
 #pragma unroll

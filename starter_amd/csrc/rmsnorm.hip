@@ -3,7 +3,7 @@
 // Arithmetic (engine/kernels/rmsnorm.py:19-36, engine/kernels/decode_fused.py:26-44;
 // Qwen3RMSNorm.forward in transformers models/qwen3/modeling_qwen3.py):
 //   total  = bf16(float(residual) + float(branch))          (add variant only)
-//   var    = sum(float(t)^2) / cols                          (f32)
+//   var    = f32(sum(float(t)^2)) / cols   (squares exact in f32, summed exactly in f64)
 //   n      = bf16(float(t) * (1 / sqrt(var + eps)))          (IEEE sqrt and divide)
 //   out    = bf16(float(n) * float(w))
 // Split-K branch: branch = bf16(((0 + p0) + p1) + ... ) in f32, in split order.
@@ -12,8 +12,8 @@
 // i, i+LPR, ..., so each wave-wide load instruction covers LPR*16 contiguous
 // bytes.  The row stays in registers between the reduction and the output, so
 // every input byte is read once and every output byte written once.  The sum
-// of squares is reduced with DPP inside 16-lane rows and ds_bpermute across
-// them; no LDS allocation and no barrier.
+// of squares is reduced in f64 with DPP inside 16-lane rows and ds_bpermute
+// across them; no LDS allocation and no barrier.
 #include "qf_device.h"
 
 namespace qf {
@@ -53,7 +53,7 @@ __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
 
   const uint4* xin = reinterpret_cast<const uint4*>(row_base<ADD>(a, r));
   float t[VPL][8];
-  float ss = 0.0f;
+  double ss = 0.0;
 
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
@@ -89,11 +89,10 @@ __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
       if (on) reinterpret_cast<uint4*>(a.total + row * a.cols)[v] = tv;
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ss += t[k][j] * t[k][j];
+    for (int j = 0; j < 8; ++j) ss += (double)(t[k][j] * t[k][j]);
   }
 
-  ss = group_sum<LPR>(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+  const float inv = inv_rms(group_sum_f64<LPR>(ss), (float)a.cols, a.eps);
 
   const uint4* wv = reinterpret_cast<const uint4*>(a.w);
   uint4* o = reinterpret_cast<uint4*>(a.out + r * a.cols);
@@ -141,14 +140,13 @@ __global__ __launch_bounds__(kBlock) void rms_scalar_kernel(RmsArgs a) {
   const int64_t row = (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
   if (row >= a.rows) return;  // wave-uniform
   const uint16_t* x = row_base<ADD>(a, row);
-  float ss = 0.0f;
+  double ss = 0.0;
   for (int64_t c = lane; c < a.cols; c += kWave) {
     const float t = scalar_value<ADD>(a, x, row, c);
     if constexpr (ADD) a.total[row * a.cols + c] = to_bf16(t);
-    ss += t * t;
+    ss += (double)(t * t);
   }
-  ss = group_sum<kWave>(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+  const float inv = inv_rms(group_sum_f64<kWave>(ss), (float)a.cols, a.eps);
   for (int64_t c = lane; c < a.cols; c += kWave) {
     const float n = from_bf16(to_bf16(scalar_value<ADD>(a, x, row, c) * inv));
     a.out[row * a.cols + c] = to_bf16(n * from_bf16(a.w[c]));

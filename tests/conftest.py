@@ -81,8 +81,17 @@ def assert_bf16_close(actual, expected, max_ulp: int = 1, atol: float = ATOL, rt
         assert exact >= min_exact, f"{what}: only {exact:.5f} bit-exact (< {min_exact})"
 
 
-def cuda_ok() -> bool:
-    return torch.cuda.is_available()
+def assert_bits_exact(actual, expected, what: str = ""):
+    """Bit-for-bit equality of two bf16 results (NaNs compared as NaN-ness,
+    since NaN payloads are not part of any contract)."""
+    a = bits(actual) if isinstance(actual, torch.Tensor) else np.asarray(actual, dtype=np.uint16)
+    e = bits(expected) if isinstance(expected, torch.Tensor) else np.asarray(expected, dtype=np.uint16)
+    assert a.shape == e.shape, (what, a.shape, e.shape)
+    nan_a, nan_e = np.isnan(O.bf16_value(a)), np.isnan(O.bf16_value(e))
+    assert np.array_equal(nan_a, nan_e), f"{what}: NaN positions differ"
+    diff = (a != e) & ~nan_a
+    assert not diff.any(), (f"{what}: {int(diff.sum())} of {a.size} elements differ, max "
+                            f"{int(O.ulp_distance(a[diff], e[diff]).max())} bf16 ulp")
 
 
 GOLDEN = Path(__file__).with_name("golden") / "golden.npz"

@@ -18,7 +18,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from conftest import O, assert_bf16_close, bits, gen, normal, tensor
+from conftest import O, assert_bf16_close, assert_bits_exact, bits, gen, normal
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
@@ -94,19 +94,19 @@ def test_decode_kernels_graph_replay_follows_position_and_inputs():
                                            bits(sin), position,
                                            np.zeros(keys.shape, np.uint16),
                                            np.zeros(keys.shape, np.uint16))
-        assert_bf16_close(outputs[0], eq, min_exact=0.99, what=f"q @ {position}")
-        assert_bf16_close(keys, ek, min_exact=0.99)
+        assert_bits_exact(outputs[0], eq, what=f"q @ {position}")
+        assert_bits_exact(keys, ek)
         assert np.array_equal(bits(values), ev)
         e_total, e_normed = O.add_rms_norm(bits(x), bits(y), bits(w), 1e-6)
         assert np.array_equal(bits(outputs[1]), e_total)
-        assert_bf16_close(outputs[2], e_normed, min_exact=0.99)
-        assert_bf16_close(outputs[3], O.silu_mul(bits(gate_up)), min_exact=0.99)
+        assert_bits_exact(outputs[2], e_normed)
+        assert_bf16_close(outputs[3], O.silu_mul(bits(gate_up)), min_exact=0.999)
         assert torch.equal(outputs[4], F.embedding(ids, table))
-        assert_bf16_close(outputs[5], O.rms_norm(bits(x), bits(w), 1e-6), min_exact=0.99)
+        assert_bits_exact(outputs[5], O.rms_norm(bits(x), bits(w), 1e-6))
         mq, mk = O.qk_norm_rope(bits(qm)[:, :, 0], bits(km)[:, :, 0], bits(qw), bits(kw),
                                 bits(cs_rows), bits(sn_rows), 1e-6, 3e-6)
-        assert_bf16_close(bits(outputs[6])[:, :, 0], mq, min_exact=0.99)
-        assert_bf16_close(bits(outputs[7])[:, :, 0], mk, min_exact=0.99)
+        assert_bits_exact(bits(outputs[6])[:, :, 0], mq)
+        assert_bits_exact(bits(outputs[7])[:, :, 0], mk)
         assert pointers == [t.data_ptr() for t in outputs]
 
 
@@ -129,8 +129,8 @@ def test_prefill_graph_replay_updates_every_prompt_slot():
         torch.cuda.synchronize()
         eq, ek, ev = O.prefill_qkv(bits(p), bits(qw), bits(kw), 1e-6, 1e-6, bits(cos), bits(sin),
                                    before_k, before_v, t)
-        assert_bf16_close(q, eq, min_exact=0.99)
-        assert_bf16_close(k, ek, min_exact=0.99)
+        assert_bits_exact(q, eq)
+        assert_bits_exact(k, ek)
         assert np.array_equal(bits(v), ev)
         assert addresses == [a.data_ptr() for a in (q, k, v)]
 
@@ -159,10 +159,10 @@ def test_module_adapters_match_the_reference_modules():
     torch.testing.assert_close(got, exact_chain, rtol=2e-2, atol=2e-3)
     torch.testing.assert_close(got, expected, rtol=3e-2, atol=3e-2)
     norm = layer.input_layernorm
-    torch.testing.assert_close(modules.FusedRMSNorm(norm)(x), norm(x), rtol=8e-3, atol=1e-5)
+    torch.testing.assert_close(modules.FusedRMSNorm(norm)(x), norm(x), rtol=1e-2, atol=1e-2)
     qn = layer.self_attn.q_norm
     q = torch.randn(2, 4, 7, 128, device=DEV).to(torch.bfloat16)
-    torch.testing.assert_close(modules.FusedRMSNorm(qn)(q), qn(q), rtol=8e-3, atol=1e-5)
+    torch.testing.assert_close(modules.FusedRMSNorm(qn)(q), qn(q), rtol=1e-2, atol=1e-2)
     ids = torch.randint(0, 127, (2, 7), device=DEV)
     tied = model.lm_head.weight is model.model.embed_tokens.weight
     emb = FusedEmbedding(model.model.embed_tokens)

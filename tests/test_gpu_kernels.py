@@ -1,9 +1,14 @@
 """GPU parity of every HIP kernel against the CPU oracle (MI355X only).
 
-The bar: the embedding gather and every copied row
-(V cache, bf16 residual sum) bit-exact; every other bf16 output within one
-bf16 ulp of the oracle and within atol/rtol 1e-2, with at least 99% of
-elements bit-identical.  Cases follow the reference tests
+The bar: the embedding gather, every copied row (V cache) and the bf16
+residual sum are bit-exact, as the BASELINE north star requires.  The norm
+and RoPE outputs are bit-exact too: kernel and oracle both sum the exact f32
+squares in f64 and round once, and every later step is a correctly rounded
+f32 operation followed by the same bf16 rounding.  SiLU*up and the rotary
+tables (f32 exp / cos / sin of different libraries) must be within one bf16
+ulp of the oracle with >= 99.9% bit-identical.  Against torch's own GPU
+formulas (a different f32 summation order) the gate is BASELINE's atol/rtol
+1e-2.  Cases follow the reference tests
 (tests/test_rmsnorm.py, tests/test_qk_norm_rope.py, tests/test_decode_step.py,
 tests/test_prefill.py) plus the five BASELINE.json configurations at full
 size, ragged/odd shapes that take the scalar paths, empty inputs, NaN-poisoned
@@ -17,7 +22,7 @@ import pytest
 import torch
 from torch.nn import functional as F
 
-from conftest import O, assert_bf16_close, bits, gen, normal, tensor
+from conftest import O, assert_bf16_close, assert_bits_exact, bits, gen, normal, tensor
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
@@ -76,8 +81,8 @@ def test_rms_norm_reference_matrix(width):
             out = rms_norm(xd, dev(w), 1e-6)
             assert out.shape == x.shape and out.is_contiguous()
             expected = O.rms_norm(bits(x.contiguous()), bits(w), 1e-6)
-            assert_bf16_close(out, expected, min_exact=0.99, what=f"{batch}x{length}x{width}")
-            torch.testing.assert_close(out, native_norm(xd, dev(w), 1e-6), rtol=8e-3, atol=1e-5)
+            assert_bits_exact(out, expected, what=f"{batch}x{length}x{width}")
+            torch.testing.assert_close(out, native_norm(xd, dev(w), 1e-6), rtol=1e-2, atol=1e-2)
             assert torch.equal(xd, before)
 
 
@@ -86,7 +91,7 @@ def test_rms_norm_config1(golden):
     x = normal((8, 2560), g=g)
     w = normal((2560,), 1.0, 0.1, g=g)
     out = rms_norm(dev(x), dev(w), 1e-6)
-    assert_bf16_close(out, O.rms_norm(bits(x), bits(w), 1e-6), min_exact=0.99)
+    assert_bits_exact(out, O.rms_norm(bits(x), bits(w), 1e-6))
     assert np.array_equal(bits(x), golden["config1_rms_norm"]["x"])
     assert_bf16_close(out, golden["config1_rms_norm"]["out"], min_exact=0.99)
 
@@ -97,7 +102,7 @@ def test_rms_norm_ragged_widths(rows, cols):
     g = gen(1)
     x, w = normal((rows, cols), g=g), normal((cols,), 1.0, 0.1, g=g)
     out = rms_norm(dev(x), dev(w), 1e-6)
-    assert_bf16_close(out, O.rms_norm(bits(x), bits(w), 1e-6), min_exact=0.99)
+    assert_bits_exact(out, O.rms_norm(bits(x), bits(w), 1e-6))
 
 
 def test_rms_norm_misaligned_view_and_known_answers():
@@ -106,7 +111,7 @@ def test_rms_norm_misaligned_view_and_known_answers():
     x = base[:, 1:]  # 2-byte offset rows: scalar path
     w = normal((2560,), 1.0, 0.1, g=g)
     out = rms_norm(dev(base)[:, 1:], dev(w), 1e-6)
-    assert_bf16_close(out, O.rms_norm(bits(x.contiguous()), bits(w), 1e-6), min_exact=0.99)
+    assert_bits_exact(out, O.rms_norm(bits(x.contiguous()), bits(w), 1e-6))
     for c in (1.0, 2.0, -4.0):
         const = torch.full((3, 2560), c, dtype=torch.bfloat16, device=DEV)
         got = rms_norm(const, dev(w), 0.0)
@@ -130,14 +135,14 @@ def test_add_rms_norm_matches_oracle(rows, cols):
     e_total, e_normed = O.add_rms_norm(bits(x), bits(y), bits(w), 1e-6)
     assert np.array_equal(bits(total), e_total)
     assert torch.equal(total, xd + yd)  # atol 0
-    assert_bf16_close(normed, e_normed, min_exact=0.99)
-    torch.testing.assert_close(normed, native_norm(xd + yd, dev(w), 1e-6), rtol=8e-3, atol=1e-5)
-    torch.testing.assert_close(normed, rms_norm(total, dev(w), 1e-6), rtol=4e-3, atol=0)
+    assert_bits_exact(normed, e_normed)
+    torch.testing.assert_close(normed, native_norm(xd + yd, dev(w), 1e-6), rtol=1e-2, atol=1e-2)
+    assert torch.equal(normed, rms_norm(total, dev(w), 1e-6))
     assert torch.equal(xd, before[0]) and torch.equal(yd, before[1])
     with pytest.raises(ValueError):
         add_rms_norm(xd.float(), yd.float(), dev(w).float(), 1e-6)
     with pytest.raises(ValueError):
-        add_rms_norm(xd, yd[:, :64].contiguous(), dev(w), 1e-6)
+        add_rms_norm(xd, yd[:, : cols // 2].contiguous(), dev(w), 1e-6)
 
 
 @pytest.mark.parametrize("splits,rows", [(1, 3), (4, 16), (8, 64), (8, 5)])
@@ -149,7 +154,7 @@ def test_add_rms_norm_split_k_partials(splits, rows):
     total, normed = add_rms_norm(dev(x), dev(partials), dev(w), 1e-6)
     e_total, e_normed = O.add_rms_norm(bits(x), partials.numpy(), bits(w), 1e-6)
     assert np.array_equal(bits(total), e_total)
-    assert_bf16_close(normed, e_normed, min_exact=0.99)
+    assert_bits_exact(normed, e_normed)
 
 
 def test_add_rms_norm_config2_chain():
@@ -166,7 +171,7 @@ def test_add_rms_norm_config2_chain():
         outs.append(normed)
     for layer in range(36):
         r_host, e_normed = O.add_rms_norm(r_host, bits(hidden[layer]), bits(w[layer]), 1e-6)
-        assert_bf16_close(outs[layer], e_normed, min_exact=0.99, what=f"layer {layer}")
+        assert_bits_exact(outs[layer], e_normed, what=f"layer {layer}")
     assert np.array_equal(bits(r_dev), r_host)
 
 
@@ -177,7 +182,7 @@ def test_add_rms_norm_config4a_full_size():
     total, normed = add_rms_norm(dev(residual), dev(hidden), dev(w), 1e-6)
     e_total, e_normed = O.add_rms_norm(bits(residual), bits(hidden), bits(w), 1e-6)
     assert np.array_equal(bits(total), e_total)
-    assert_bf16_close(normed, e_normed, min_exact=0.99)
+    assert_bits_exact(normed, e_normed)
 
 
 # ----------------------------------------------------------------- silu_mul
@@ -193,7 +198,7 @@ def test_silu_mul_matches_oracle(rows, cols):
     out = silu_mul(dev(gate_up))
     assert tuple(out.shape) == (rows, cols)
     assert bool(torch.isfinite(out).all())
-    assert_bf16_close(out, O.silu_mul(bits(gate_up)), min_exact=0.99)
+    assert_bf16_close(out, O.silu_mul(bits(gate_up)), min_exact=0.999)
     gate, up = dev(gate_up).chunk(2, dim=-1)
     torch.testing.assert_close(out, F.silu(gate) * up, rtol=1e-2, atol=1e-3)
     if rows:
@@ -218,7 +223,7 @@ def test_silu_mul_misaligned_scalar_path():
     out2 = silu_mul(shifted)  # 2-byte offset: scalar path
     expected = O.silu_mul(bits(base[:, 1:].contiguous()))
     assert np.array_equal(bits(out), bits(out2))
-    assert_bf16_close(out2, expected, min_exact=0.99)
+    assert_bf16_close(out2, expected, min_exact=0.999)
 
 
 # ------------------------------------------------------------- qk_norm_rope
@@ -249,8 +254,8 @@ def test_qk_norm_rope_reference_matrix():
                                             bits(c), bits(s), 1e-6, 3e-6)
                     what = f"b{batch} shared{shared} p{position} strided{strided}"
                     assert oq.is_contiguous() and ok.is_contiguous()
-                    assert_bf16_close(bits(oq)[:, :, 0], eq, min_exact=0.99, what=what)
-                    assert_bf16_close(bits(ok)[:, :, 0], ek, min_exact=0.99, what=what)
+                    assert_bits_exact(bits(oq)[:, :, 0], eq, what=what)
+                    assert_bits_exact(bits(ok)[:, :, 0], ek, what=what)
                     nq_ref, nk_ref = apply_rope(native_norm(qd, dev(qw), 1e-6),
                                                 native_norm(kd, dev(kw), 3e-6), dev(c), dev(s))
                     torch.testing.assert_close(oq, nq_ref, rtol=0.02, atol=0.02)
@@ -287,8 +292,8 @@ def test_qk_norm_rope_config3():
                           dev(kw), c, s, 1e-6, 1e-6)
     eq, ek = O.qk_norm_rope(bits(q)[:, 0], bits(k)[:, 0], bits(qw), bits(kw), bits(c), bits(s),
                             1e-6, 1e-6)
-    assert_bf16_close(bits(oq)[:, :, 0], eq, min_exact=0.99)
-    assert_bf16_close(bits(ok)[:, :, 0], ek, min_exact=0.99)
+    assert_bits_exact(bits(oq)[:, :, 0], eq)
+    assert_bits_exact(bits(ok)[:, :, 0], ek)
 
 
 # ------------------------------------------------------- qkv_norm_rope_cache
@@ -312,8 +317,8 @@ def test_qkv_norm_rope_cache_values_slots_and_untouched_capacity(batch, heads, k
         eq, ek, ev = O.qkv_norm_rope_cache(bits(qkv), bits(qw), bits(kw), 1e-6, 3e-6, bits(cos),
                                            bits(sin), position, bits(keys), bits(values))
         assert tuple(q.shape) == (batch, heads, 1, 128) and q.is_contiguous()
-        assert_bf16_close(q, eq, min_exact=0.99)
-        assert_bf16_close(bits(keys)[:, :, position], ek[:, :, position], min_exact=0.99)
+        assert_bits_exact(q, eq)
+        assert_bits_exact(bits(keys)[:, :, position], ek[:, :, position])
         assert np.array_equal(bits(values)[:, :, position], ev[:, :, position])
         untouched = torch.arange(capacity, device=DEV) != position
         assert bool(keys[:, :, untouched].isnan().all())
@@ -360,8 +365,8 @@ def test_qkv_split_k_partials_and_position_guard():
                             keys, values)
     eq, ek, ev = O.qkv_norm_rope_cache(partials.numpy(), bits(qw), bits(kw), 1e-6, 1e-6,
                                        bits(cos), bits(sin), 37, bits(keys), bits(values))
-    assert_bf16_close(q, eq, min_exact=0.99)
-    assert_bf16_close(keys, ek, min_exact=0.99)
+    assert_bits_exact(q, eq)
+    assert_bits_exact(keys, ek)
     assert np.array_equal(bits(values), ev)
     # Out-of-range positions (forced from the host) write nothing and give NaN Q.
     for bad in (-1, capacity, 1 << 40):
@@ -391,8 +396,8 @@ def test_prefill_qkv_matches_oracle(b, t, c, nq, nk):
     eq, ek, ev = O.prefill_qkv(bits(p), bits(qw), bits(kw), 1e-6, 3e-6, bits(cos), bits(sin),
                                bits(k), bits(v), t)
     assert tuple(q.shape) == (b, t, nq, 128)
-    assert_bf16_close(q, eq, min_exact=0.99)
-    assert_bf16_close(bits(k)[:, :, :t], ek[:, :, :t], min_exact=0.99)
+    assert_bits_exact(q, eq)
+    assert_bits_exact(bits(k)[:, :, :t], ek[:, :, :t])
     assert np.array_equal(bits(v)[:, :, :t], ev[:, :, :t])
     assert bool(torch.isnan(k[:, :, t:]).all() & torch.isnan(v[:, :, t:]).all())
     assert torch.equal(pd, before)
@@ -410,8 +415,8 @@ def test_prefill_qkv_config4b_full_size():
     q = prefill_qkv(dev(p), dev(qw), dev(kw), 1e-6, 1e-6, dev(cos), dev(sin), k, v, t)
     eq, ek, ev = O.prefill_qkv(bits(p), bits(qw), bits(kw), 1e-6, 1e-6, bits(cos), bits(sin),
                                bits(k), bits(v), t)
-    assert_bf16_close(q, eq, min_exact=0.99)
-    assert_bf16_close(k, ek, min_exact=0.99)
+    assert_bits_exact(q, eq)
+    assert_bits_exact(k, ek)
     assert np.array_equal(bits(v), ev)
 
 
