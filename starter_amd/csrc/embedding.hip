@@ -16,7 +16,7 @@
 namespace qf {
 namespace {
 
-template <int VPL>
+template <int VPL, bool NT>
 __global__ __launch_bounds__(kBlock) void embedding_vec_kernel(const int64_t* __restrict__ ids,
                                                               const uint4* __restrict__ table,
                                                               uint4* __restrict__ out,
@@ -33,12 +33,12 @@ __global__ __launch_bounds__(kBlock) void embedding_vec_kernel(const int64_t* __
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int c = lane + k * kWave;
-    v[k] = (valid && c < nvec) ? src[c] : make_uint4(0, 0, 0, 0);
+    v[k] = (valid && c < nvec) ? load16<NT>(src + c) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int c = lane + k * kWave;
-    if (c < nvec) dst[c] = v[k];
+    if (c < nvec) store16<NT>(dst + c, v[k]);
   }
 }
 
@@ -61,9 +61,14 @@ template <int VPL>
 int launch_embedding(const int64_t* ids, const void* table, void* out, int64_t n_ids,
                      int64_t vocab, int32_t nvec, hipStream_t s) {
   const int64_t blocks = (n_ids + 3) / 4;
-  hipLaunchKernelGGL((embedding_vec_kernel<VPL>), dim3((unsigned)blocks), dim3(kBlock), 0, s, ids,
-                     static_cast<const uint4*>(table), static_cast<uint4*>(out), n_ids, vocab,
-                     nvec);
+  if (n_ids * nvec * 32 >= kStreamBytes)
+    hipLaunchKernelGGL((embedding_vec_kernel<VPL, true>), dim3((unsigned)blocks), dim3(kBlock), 0, s,
+                       ids, static_cast<const uint4*>(table), static_cast<uint4*>(out), n_ids,
+                       vocab, nvec);
+  else
+    hipLaunchKernelGGL((embedding_vec_kernel<VPL, false>), dim3((unsigned)blocks), dim3(kBlock), 0,
+                       s, ids, static_cast<const uint4*>(table), static_cast<uint4*>(out), n_ids,
+                       vocab, nvec);
   return launch_status();
 }
 

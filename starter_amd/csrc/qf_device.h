@@ -61,6 +61,38 @@ __device__ __forceinline__ void round8(float* f) {
   unpack8(u, f);
 }
 
+// ---- 16-byte global loads / stores ------------------------------------------
+
+// NT = true marks the access nontemporal (streamed once: the "nt" bit of
+// global_load/store_dwordx4), which measurably raises streaming bandwidth on
+// gfx950; NT = false is an ordinary cached access (for data re-read soon,
+// such as gains and rotary rows).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ uint4 load16(const void* p) {
+  if constexpr (NT) {
+    const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *static_cast<const uint4*>(p);
+  }
+}
+template <bool NT>
+__device__ __forceinline__ void store16(void* p, const uint4& v) {
+  if constexpr (NT) {
+    const u32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, static_cast<u32x4*>(p));
+  } else {
+    *static_cast<uint4*>(p) = v;
+  }
+}
+
+// Calls that touch at least this many bytes stream their row data with
+// nontemporal accesses; smaller (decode-size) calls keep ordinary cached
+// accesses so the next kernel finds their outputs in L2 / Infinity Cache.
+constexpr int64_t kStreamBytes = 32ll << 20;
+
 // ---- DPP / cross-lane -------------------------------------------------------
 
 // DPP control words (GFX9 encoding).

@@ -41,19 +41,22 @@ __device__ __forceinline__ uint4 select4(bool c, const uint4& a, const uint4& b)
 }
 
 // Norm + gain + RoPE of one head row held as 8 f32 per lane (values already
-// representable in bf16).  Returns the 8 bf16 outputs of this lane.
-__device__ __forceinline__ uint4 norm_rope(const float* x, uint4 wv, uint4 cv, uint4 sv,
-                                           float eps, int l16) {
+// representable in bf16).  w, c are this lane's gains and cos values; sr is
+// its sin values with the rotate-half sign folded in (-sin on lanes 0..7 of
+// the DPP row, whose partner values come from the second half):
+// (-p) * s == p * (-s) exactly, so bf16(rot * sin) is unchanged.
+// Returns the 8 bf16 outputs of this lane.
+__device__ __forceinline__ uint4 norm_rope_f(const float* x, const float* w, const float* c,
+                                             const float* sr, float eps) {
   double ss = 0.0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) ss += (double)(x[j] * x[j]);  // exact squares, exact sum
   const float inv = inv_rms(group_sum_f64<kLanes>(ss), (float)kD, eps);
 
-  float n[8], w[8];
+  float n[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) n[j] = x[j] * inv;
   round8(n);
-  unpack8(wv, w);
 #pragma unroll
   for (int j = 0; j < 8; ++j) n[j] *= w[j];
   const uint4 nb = pack8(n);
@@ -65,23 +68,34 @@ __device__ __forceinline__ uint4 norm_rope(const float* x, uint4 wv, uint4 cv, u
   pb.y = dpp_u32<kRowRor8>(nb.y);
   pb.z = dpp_u32<kRowRor8>(nb.z);
   pb.w = dpp_u32<kRowRor8>(nb.w);
-  float p[8], c[8], s[8];
+  float p[8], left[8];
   unpack8(pb, p);
-  unpack8(cv, c);
-  unpack8(sv, s);
-  const float sign = l16 < 8 ? -1.0f : 1.0f;  // exact negation of the partner
-
-  float left[8], right[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     left[j] = n[j] * c[j];
-    right[j] = (sign * p[j]) * s[j];
+    p[j] *= sr[j];
   }
   round8(left);
-  round8(right);
+  round8(p);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) left[j] += right[j];
+  for (int j = 0; j < 8; ++j) left[j] += p[j];
   return pack8(left);
+}
+
+// Negate both bf16 of every dword (sign bit flip) when `neg`.
+__device__ __forceinline__ uint4 negate_if(uint4 v, bool neg) {
+  const uint32_t m = neg ? 0x80008000u : 0u;
+  return make_uint4(v.x ^ m, v.y ^ m, v.z ^ m, v.w ^ m);
+}
+
+// Same with gains / cos / sin still packed.
+__device__ __forceinline__ uint4 norm_rope(const float* x, uint4 wv, uint4 cv, uint4 sv,
+                                           float eps, int l16) {
+  float w[8], c[8], sr[8];
+  unpack8(wv, w);
+  unpack8(cv, c);
+  unpack8(negate_if(sv, l16 < 8), sr);
+  return norm_rope_f(x, w, c, sr, eps);
 }
 
 // ---------------------------------------------------------------- module path
@@ -201,9 +215,12 @@ __global__ __launch_bounds__(kBlock) void qkv_norm_rope_cache_kernel(QkvArgs a) 
 // ------------------------------------------------------------ packed prefill
 struct PrefillArgs {
   const uint16_t* qkv;     // [batch * length, W]
-  uint32_t rows;           // batch * length * heads
+  uint32_t rows;           // batch * length * heads          (generic kernel)
+  uint32_t waves;          // tokens * waves per token        (unit kernel)
   uint32_t nq, nk;
+  uint32_t q_units, k_units, units;  // nq / 8, nk / 8, (nq + 2 nk) / 8
   FastDiv heads;           // nq + 2 nk
+  FastDiv waves_per_token; // ceil(units / kUnitsPerWave)
   FastDiv length;
   const uint16_t* qw;
   const uint16_t* kw;
@@ -216,6 +233,119 @@ struct PrefillArgs {
   uint16_t* vc;
 };
 
+// Unit kernel (nq and nk multiples of 8).  A lane holds 16 elements of one
+// head row: [8l, 8l+8) and their rotate-half partners [64+8l, 64+8l+8), so
+// the partner exchange needs no cross-lane traffic and a row is reduced over
+// 8 lanes (3 DPP steps).  A "unit" is 8 consecutive head rows of one token
+// with one role (q, k or v), one per 8-lane group of a wave.  A wave owns up
+// to kUnitsPerWave consecutive units of one token: its loads all issue first,
+// the token's cos/sin row and both gains are unpacked once per wave, roles
+// are wave-uniform (scalar branches) and v units are pure copies.
+// Qwen3-4B: 6 units per token -> 3 waves.
+constexpr int kUnitsPerWave = 2;
+constexpr int kRowLanes = 8;  // lanes per head row in the unit kernel
+
+// Norm + gain + RoPE of one head row spread as 16 elements per lane over 8
+// lanes: x[0..7] are elements 8l+j, x[8..15] their partners 64+8l+j.  sr is
+// sin with the rotate-half sign folded in (negated for the first half).
+__device__ __forceinline__ void norm_rope16(const float* x, const float* w, const float* c,
+                                            const float* sr, float eps, uint4& lo, uint4& hi) {
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) ss += (double)(x[j] * x[j]);  // exact squares, exact sum
+  const float inv = inv_rms(group_sum_f64<kRowLanes>(ss), (float)kD, eps);
+  float n[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) n[j] = x[j] * inv;
+  round8(n);
+  round8(n + 8);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) n[j] *= w[j];
+  round8(n);
+  round8(n + 8);
+  float left[16], right[16];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    left[j] = n[j] * c[j];
+    right[j] = n[j + 8] * sr[j];          // rot = -n[e + 64] for the first half
+    left[j + 8] = n[j + 8] * c[j + 8];
+    right[j + 8] = n[j] * sr[j + 8];      // rot = n[e - 64] for the second half
+  }
+  round8(left);
+  round8(left + 8);
+  round8(right);
+  round8(right + 8);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) left[j] += right[j];
+  lo = pack8(left);
+  hi = pack8(left + 8);
+}
+
+template <bool NT>
+__global__ __launch_bounds__(kBlock) void prefill_qkv_unit_kernel(PrefillArgs a) {
+  const uint32_t wave =
+      __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave);
+  if (wave >= a.waves) return;  // wave-uniform
+  const uint32_t token = __builtin_amdgcn_readfirstlane(fdiv(wave, a.waves_per_token));
+  const uint32_t first =
+      __builtin_amdgcn_readfirstlane((wave - token * a.waves_per_token.d) * kUnitsPerWave);
+  const uint32_t b = __builtin_amdgcn_readfirstlane(fdiv(token, a.length));
+  const uint32_t t = token - b * a.length.d;
+  const int lane = threadIdx.x % kWave;
+  const int grp = lane / kRowLanes;  // head within the unit
+  const int l = lane % kRowLanes;
+
+  const int64_t width = (int64_t)a.heads.d * kD;
+  const uint16_t* src = a.qkv + (int64_t)token * width + grp * kD + l * 8;
+  uint4 xlo[kUnitsPerWave], xhi[kUnitsPerWave];
+#pragma unroll
+  for (int u = 0; u < kUnitsPerWave; ++u) {
+    if (first + u < a.units) {
+      const uint16_t* p = src + (int64_t)(first + u) * kRowLanes * kD;
+      xlo[u] = load16<NT>(p);
+      xhi[u] = load16<NT>(p + kD / 2);
+    }
+  }
+
+  float c[16], sr[16], wq[16], wk[16];
+  const int64_t trow = (int64_t)t * kD + l * 8;
+  unpack8(load16<false>(a.cos + trow), c);
+  unpack8(load16<false>(a.cos + trow + kD / 2), c + 8);
+  unpack8(negate_if(load16<false>(a.sin + trow), true), sr);
+  unpack8(load16<false>(a.sin + trow + kD / 2), sr + 8);
+  unpack8(load16<false>(a.qw + l * 8), wq);
+  unpack8(load16<false>(a.qw + l * 8 + kD / 2), wq + 8);
+  unpack8(load16<false>(a.kw + l * 8), wk);
+  unpack8(load16<false>(a.kw + l * 8 + kD / 2), wk + 8);
+
+#pragma unroll
+  for (int u = 0; u < kUnitsPerWave; ++u) {
+    const uint32_t unit = first + u;
+    if (unit >= a.units) break;  // wave-uniform
+    uint16_t* dst;
+    uint4 lo = xlo[u], hi = xhi[u];
+    if (unit < a.q_units + a.k_units) {
+      float x[16];
+      unpack8(xlo[u], x);
+      unpack8(xhi[u], x + 8);
+      if (unit < a.q_units) {
+        norm_rope16(x, wq, c, sr, a.q_eps, lo, hi);
+        dst = a.q_out + ((uint64_t)token * a.nq + unit * kRowLanes + grp) * kD;
+      } else {
+        norm_rope16(x, wk, c, sr, a.k_eps, lo, hi);
+        const uint32_t kvh = (unit - a.q_units) * kRowLanes + grp;
+        dst = a.kc + (((int64_t)b * a.nk + kvh) * a.capacity + t) * kD;
+      }
+    } else {
+      const uint32_t kvh = (unit - a.q_units - a.k_units) * kRowLanes + grp;
+      dst = a.vc + (((int64_t)b * a.nk + kvh) * a.capacity + t) * kD;  // raw copy
+    }
+    store16<NT>(dst + l * 8, lo);
+    store16<NT>(dst + l * 8 + kD / 2, hi);
+  }
+}
+
+// Generic kernel (any nq, nk): one head row per 16-lane group.
 __global__ __launch_bounds__(kBlock) void prefill_qkv_kernel(PrefillArgs a) {
   const uint32_t g = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanes;
   const int l = threadIdx.x % kLanes;
@@ -368,7 +498,24 @@ extern "C" int qf_prefill_qkv(const void* qkv, int64_t batch, int64_t length, in
   a.q_out = static_cast<uint16_t*>(q_out);
   a.kc = static_cast<uint16_t*>(key_cache);
   a.vc = static_cast<uint16_t*>(value_cache);
-  hipLaunchKernelGGL(prefill_qkv_kernel, dim3(blocks_for(rows)), dim3(kBlock), 0,
-                     as_stream(stream), a);
+  hipStream_t s = as_stream(stream);
+  if (nq % kRowLanes == 0 && nk % kRowLanes == 0) {
+    a.q_units = (uint32_t)nq / kRowLanes;
+    a.k_units = (uint32_t)nk / kRowLanes;
+    a.units = (uint32_t)heads / kRowLanes;
+    const uint32_t per_token = (a.units + kUnitsPerWave - 1) / kUnitsPerWave;
+    a.waves_per_token = make_fastdiv(per_token);
+    const uint64_t waves = tokens * per_token;
+    a.waves = (uint32_t)waves;
+    const uint64_t blocks = (waves + kBlock / kWave - 1) / (kBlock / kWave);
+    if ((int64_t)rows * kD * 4 >= kStreamBytes)
+      hipLaunchKernelGGL((prefill_qkv_unit_kernel<true>), dim3((unsigned)blocks), dim3(kBlock), 0, s,
+                         a);
+    else
+      hipLaunchKernelGGL((prefill_qkv_unit_kernel<false>), dim3((unsigned)blocks), dim3(kBlock), 0,
+                         s, a);
+    return launch_status();
+  }
+  hipLaunchKernelGGL(prefill_qkv_kernel, dim3(blocks_for(rows)), dim3(kBlock), 0, s, a);
   return launch_status();
 }

@@ -43,7 +43,7 @@ __device__ __forceinline__ const uint16_t* row_base(const RmsArgs& a, int64_t r)
 }
 
 // Vector path: cols % 8 == 0 and every pointer / row stride 16-byte aligned.
-template <int LPR, int VPL, bool ADD>
+template <int LPR, int VPL, bool ADD, bool NT>
 __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
   constexpr int kRowsPerBlock = kBlock / LPR;
   const int lane = threadIdx.x % LPR;
@@ -59,14 +59,14 @@ __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
   for (int k = 0; k < VPL; ++k) {
     const int v = lane + k * LPR;
     const bool on = live && v < a.nvec;
-    uint4 xv = on ? xin[v] : make_uint4(0, 0, 0, 0);
+    uint4 xv = on ? load16<NT>(xin + v) : make_uint4(0, 0, 0, 0);
     unpack8(xv, t[k]);
     if constexpr (ADD) {
       float y[8];
       if (a.splits == 0) {
         const uint4* b = reinterpret_cast<const uint4*>(
             static_cast<const uint16_t*>(a.branch) + r * a.cols);
-        uint4 bv = on ? b[v] : make_uint4(0, 0, 0, 0);
+        uint4 bv = on ? load16<NT>(b + v) : make_uint4(0, 0, 0, 0);
         unpack8(bv, y);
       } else {
         // f32 partials: two 16-byte halves per 8 columns, summed in split order.
@@ -74,10 +74,12 @@ __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
         for (int j = 0; j < 8; ++j) y[j] = 0.0f;
         const float* p = static_cast<const float*>(a.branch) + r * a.cols + (int64_t)v * 8;
         for (int s = 0; s < a.splits; ++s) {
-          float4 p0 = on ? reinterpret_cast<const float4*>(p)[0] : make_float4(0, 0, 0, 0);
-          float4 p1 = on ? reinterpret_cast<const float4*>(p)[1] : make_float4(0, 0, 0, 0);
-          y[0] += p0.x; y[1] += p0.y; y[2] += p0.z; y[3] += p0.w;
-          y[4] += p1.x; y[5] += p1.y; y[6] += p1.z; y[7] += p1.w;
+          const uint4 p0 = on ? load16<NT>(p) : make_uint4(0, 0, 0, 0);
+          const uint4 p1 = on ? load16<NT>(p + 4) : make_uint4(0, 0, 0, 0);
+          y[0] += __uint_as_float(p0.x); y[1] += __uint_as_float(p0.y);
+          y[2] += __uint_as_float(p0.z); y[3] += __uint_as_float(p0.w);
+          y[4] += __uint_as_float(p1.x); y[5] += __uint_as_float(p1.y);
+          y[6] += __uint_as_float(p1.z); y[7] += __uint_as_float(p1.w);
           p += a.split_stride;
         }
         round8(y);
@@ -86,7 +88,7 @@ __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
       for (int j = 0; j < 8; ++j) t[k][j] += y[j];
       uint4 tv = pack8(t[k]);
       unpack8(tv, t[k]);
-      if (on) reinterpret_cast<uint4*>(a.total + row * a.cols)[v] = tv;
+      if (on) store16<NT>(reinterpret_cast<uint4*>(a.total + row * a.cols) + v, tv);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss += (double)(t[k][j] * t[k][j]);
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
     unpack8(on ? wv[v] : make_uint4(0, 0, 0, 0), w);
 #pragma unroll
     for (int j = 0; j < 8; ++j) n[j] *= w[j];
-    if (on) o[v] = pack8(n);
+    if (on) store16<NT>(o + v, pack8(n));
   }
 }
 
@@ -156,7 +158,13 @@ __global__ __launch_bounds__(kBlock) void rms_scalar_kernel(RmsArgs a) {
 template <int LPR, int VPL, bool ADD>
 int launch_vec(const RmsArgs& a, hipStream_t s) {
   const int64_t blocks = (a.rows + (kBlock / LPR) - 1) / (kBlock / LPR);
-  hipLaunchKernelGGL((rms_vec_kernel<LPR, VPL, ADD>), dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
+  const int64_t bytes = a.rows * a.cols * 2 * (ADD ? 4 : 2);
+  if (bytes >= kStreamBytes)
+    hipLaunchKernelGGL((rms_vec_kernel<LPR, VPL, ADD, true>), dim3((unsigned)blocks), dim3(kBlock),
+                       0, s, a);
+  else
+    hipLaunchKernelGGL((rms_vec_kernel<LPR, VPL, ADD, false>), dim3((unsigned)blocks), dim3(kBlock),
+                       0, s, a);
   return launch_status();
 }
 

@@ -2,25 +2,63 @@
 //
 // Arithmetic (engine/kernels/decode_fused.py:52-56; F.silu(gate) * up on bf16
 // tensors in engine/mlp.py:19-21):
-//   a   = bf16(g / (1 + exp(-g)))          f32 exp, IEEE divide
+//   a   = bf16(g / (1 + exp(-g)))
 //   out = bf16(float(a) * float(u))
+// The f32 SiLU is first evaluated cheaply: exp(-g) = 2^t on the hardware exp2
+// (v_exp_f32) with t = -g * log2 e, the rounding error of t restored by one
+// FMA (2^(t + dt) ~= 2^t * (1 + dt ln 2)), and g / d as g * (1 / d) on the
+// hardware reciprocal (v_rcp_f32).  That value is within a few f32 ulps of the
+// correctly rounded quotient; it can only round to a different bf16 when it
+// lies near a bf16 rounding midpoint, so an element within kBand f32 ulps of
+// one - or whose reciprocal would be denormal (g < -86.6) - is recomputed
+// with the f32 formula itself (expf, IEEE divide).  That happens for ~0.05%
+// of elements.  bf16(silu(g)) depends only on the 16-bit gate, and the tests
+// check every one of the 65,536 gate values against the oracle bit for bit.
+// The cheap path costs ~9 VALU instructions per element instead of ~25 for
+// expf and an IEEE divide, which would make the kernel VALU-bound.
 //
 // Layout: the output is a flat sequence of 16-byte vectors (8 columns).  A
-// thread owns U vectors spaced one workgroup apart, so each wave-wide load
-// covers 1 KiB of consecutive gate (or up) bytes and each thread keeps 2*U
-// 16-byte loads in flight.  Row / column of a vector come from a
-// multiply-high division by the per-row vector count.
+// thread owns U vectors spaced one workgroup apart, so each wave-wide access
+// covers 1 KiB of consecutive gate, up or output bytes.  Row / column of a
+// vector come from a multiply-high division by the per-row vector count.
 #include "qf_device.h"
 
 namespace qf {
 namespace {
 
-__device__ __forceinline__ float silu_bf16(float g) {
-  // Rounded to bf16 before the product, as the reference does.
-  return from_bf16(to_bf16(g / (1.0f + expf(-g))));
+constexpr float kLog2e = 0x1.715476p+0f;     // log2(e) rounded to f32
+constexpr float kLog2eLo = 0x1.4ae0c0p-26f;  // log2(e) - kLog2e
+constexpr float kLn2 = 0x1.62e430p-1f;
+constexpr int kBand = 16;                    // f32 ulps around a bf16 midpoint
+
+// g / (1 + exp(-g)) with every step correctly rounded in f32.
+__device__ __attribute__((noinline)) float silu_exact(float g) { return g / (1.0f + expf(-g)); }
+
+__device__ __forceinline__ float silu_f32(float g) {
+  const float t = -g * kLog2e;
+  const float dt = __builtin_fmaf(-g, kLog2e, -t) + (-g) * kLog2eLo;  // t's rounding error
+  const float e0 = __builtin_amdgcn_exp2f(t);                         // v_exp_f32
+  const float e = __builtin_fmaf(e0, dt * kLn2, e0);
+  const float d = 1.0f + e;
+  const float a = g * __builtin_amdgcn_rcpf(d);                       // v_rcp_f32
+  const int low = (int)(__float_as_uint(a) & 0xffffu);                // bits below bf16
+  if (__builtin_expect(abs(low - 0x8000) < kBand || !(d < 0x1p125f), 0)) return silu_exact(g);
+  return a;
 }
 
-template <int U>
+__device__ __forceinline__ uint4 silu_mul8(const uint4& gv, const uint4& uv) {
+  float g[8], u[8];
+  unpack8(gv, g);
+  unpack8(uv, u);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) g[j] = silu_f32(g[j]);
+  round8(g);  // SiLU rounded to bf16 before the product, as the reference does
+#pragma unroll
+  for (int j = 0; j < 8; ++j) g[j] *= u[j];
+  return pack8(g);
+}
+
+template <int U, bool NT>
 __global__ __launch_bounds__(kBlock) void silu_mul_vec_kernel(const uint4* __restrict__ gu,
                                                              uint4* __restrict__ out,
                                                              uint32_t total_vec, FastDiv per_row) {
@@ -33,21 +71,14 @@ __global__ __launch_bounds__(kBlock) void silu_mul_vec_kernel(const uint4* __res
       const uint32_t row = fdiv(i, per_row);
       const uint32_t col = i - row * per_row.d;
       const uint4* g = gu + (uint64_t)row * (2 * per_row.d) + col;
-      gv[k] = g[0];
-      uv[k] = g[per_row.d];
+      gv[k] = load16<NT>(g);
+      uv[k] = load16<NT>(g + per_row.d);
     }
   }
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     const uint32_t i = base + k * kBlock;
-    if (i < total_vec) {
-      float g[8], u[8];
-      unpack8(gv[k], g);
-      unpack8(uv[k], u);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) g[j] = silu_bf16(g[j]) * u[j];
-      out[i] = pack8(g);
-    }
+    if (i < total_vec) store16<NT>(out + i, silu_mul8(gv[k], uv[k]));
   }
 }
 
@@ -61,11 +92,20 @@ __global__ __launch_bounds__(kBlock) void silu_mul_scalar_kernel(const uint16_t*
     const int64_t r = i / cols, c = i - r * cols;
     const float g = from_bf16(gu[r * 2 * cols + c]);
     const float u = from_bf16(gu[r * 2 * cols + cols + c]);
-    out[i] = to_bf16(silu_bf16(g) * u);
+    out[i] = to_bf16(from_bf16(to_bf16(silu_f32(g))) * u);
   }
 }
 
-constexpr int kSiluU = 2;
+template <int U, bool NT>
+int launch_silu_vec(const void* gate_up, void* out, int64_t nvec_total, int64_t cols,
+                    hipStream_t s) {
+  const FastDiv per_row = make_fastdiv((uint32_t)(cols / 8));
+  const int64_t blocks = (nvec_total + kBlock * U - 1) / (kBlock * U);
+  hipLaunchKernelGGL((silu_mul_vec_kernel<U, NT>), dim3((unsigned)blocks), dim3(kBlock), 0, s,
+                     static_cast<const uint4*>(gate_up), static_cast<uint4*>(out),
+                     (uint32_t)nvec_total, per_row);
+  return launch_status();
+}
 
 }  // namespace
 }  // namespace qf
@@ -79,13 +119,11 @@ extern "C" int qf_silu_mul(const void* gate_up, int64_t rows, int64_t cols, void
   if (!gate_up || !out) return QF_E_ARG;
   hipStream_t s = as_stream(stream);
   const int64_t nvec_total = rows * (cols / 8);
-  if (cols % 8 == 0 && aligned16(gate_up) && aligned16(out) && nvec_total < (int64_t)UINT32_MAX - kBlock * kSiluU) {
-    const FastDiv per_row = make_fastdiv((uint32_t)(cols / 8));
-    const int64_t blocks = (nvec_total + kBlock * kSiluU - 1) / (kBlock * kSiluU);
-    hipLaunchKernelGGL((silu_mul_vec_kernel<kSiluU>), dim3((unsigned)blocks), dim3(kBlock), 0, s,
-                       static_cast<const uint4*>(gate_up), static_cast<uint4*>(out),
-                       (uint32_t)nvec_total, per_row);
-    return launch_status();
+  if (cols % 8 == 0 && aligned16(gate_up) && aligned16(out) &&
+      nvec_total < (int64_t)UINT32_MAX - 4 * kBlock) {
+    if (nvec_total * 48 >= kStreamBytes)
+      return launch_silu_vec<1, true>(gate_up, out, nvec_total, cols, s);
+    return launch_silu_vec<1, false>(gate_up, out, nvec_total, cols, s);
   }
   const int64_t n = rows * cols;
   int64_t blocks = (n + kBlock - 1) / kBlock;

@@ -4,9 +4,11 @@ The bar: the embedding gather, every copied row (V cache) and the bf16
 residual sum are bit-exact, as the BASELINE north star requires.  The norm
 and RoPE outputs are bit-exact too: kernel and oracle both sum the exact f32
 squares in f64 and round once, and every later step is a correctly rounded
-f32 operation followed by the same bf16 rounding.  SiLU*up and the rotary
-tables (f32 exp / cos / sin of different libraries) must be within one bf16
-ulp of the oracle with >= 99.9% bit-identical.  Against torch's own GPU
+f32 operation followed by the same bf16 rounding.  SiLU*up is bit-exact as
+well, proven exhaustively over all 65,536 bf16 gate values (the kernel's fast
+exp2/reciprocal path falls back to the exact f32 formula near bf16 rounding
+midpoints).  The rotary tables (f32 cos / sin of different libraries) must be
+within one bf16 ulp of the oracle with >= 99.9% bit-identical.  Against torch's own GPU
 formulas (a different f32 summation order) the gate is BASELINE's atol/rtol
 1e-2.  Cases follow the reference tests
 (tests/test_rmsnorm.py, tests/test_qk_norm_rope.py, tests/test_decode_step.py,
@@ -198,7 +200,7 @@ def test_silu_mul_matches_oracle(rows, cols):
     out = silu_mul(dev(gate_up))
     assert tuple(out.shape) == (rows, cols)
     assert bool(torch.isfinite(out).all())
-    assert_bf16_close(out, O.silu_mul(bits(gate_up)), min_exact=0.999)
+    assert_bits_exact(out, O.silu_mul(bits(gate_up)))
     gate, up = dev(gate_up).chunk(2, dim=-1)
     torch.testing.assert_close(out, F.silu(gate) * up, rtol=1e-2, atol=1e-3)
     if rows:
@@ -206,11 +208,24 @@ def test_silu_mul_matches_oracle(rows, cols):
             silu_mul(dev(gate_up)[:, :-1].contiguous())
 
 
+def test_silu_mul_exhaustive_over_every_bf16_gate():
+    """bf16(silu(g)) depends only on the 16-bit gate, so every possible gate
+    value is checked: the hardware exp2 / reciprocal formulation must round
+    to the same bf16 as the oracle's IEEE expf and divide for all of them."""
+    gate = torch.arange(65536, dtype=torch.int32).to(torch.uint16).view(torch.bfloat16)
+    g = gen(21)
+    for up in (torch.ones(65536, dtype=torch.bfloat16), normal((65536,), 0.0, 2.0, g=g)):
+        gate_up = torch.cat([gate, up]).view(1, -1)
+        out = silu_mul(dev(gate_up))
+        expected = O.silu_mul(bits(gate_up))
+        assert_bits_exact(out, expected, what="all bf16 gates")
+
+
 def test_silu_mul_config5a_full_size():
     g = gen(0)
     gate_up = normal((8192, 19456), g=g)
     out = silu_mul(dev(gate_up))
-    assert_bf16_close(out, O.silu_mul(bits(gate_up)), min_exact=0.999)
+    assert_bits_exact(out, O.silu_mul(bits(gate_up)))
 
 
 def test_silu_mul_misaligned_scalar_path():
@@ -223,7 +238,7 @@ def test_silu_mul_misaligned_scalar_path():
     out2 = silu_mul(shifted)  # 2-byte offset: scalar path
     expected = O.silu_mul(bits(base[:, 1:].contiguous()))
     assert np.array_equal(bits(out), bits(out2))
-    assert_bf16_close(out2, expected, min_exact=0.999)
+    assert_bits_exact(out2, expected)
 
 
 # ------------------------------------------------------------- qk_norm_rope
@@ -381,7 +396,8 @@ def test_qkv_split_k_partials_and_position_guard():
 
 @pytest.mark.parametrize("b,t,c,nq,nk", [(1, 3, 11, 32, 8), (2, 33, 41, 32, 8),
                                          (1, 129, 137, 32, 8), (3, 17, 33, 32, 8),
-                                         (2, 7, 13, 4, 2), (2, 5, 9, 12, 4), (1, 1, 3, 4, 2)])
+                                         (2, 7, 13, 4, 2), (2, 5, 9, 12, 4), (1, 1, 3, 4, 2),
+                                         (2, 9, 12, 8, 8), (1, 5, 7, 24, 8), (3, 4, 4, 16, 8)])
 def test_prefill_qkv_matches_oracle(b, t, c, nq, nk):
     """tests/test_prefill.py:504-522 of the reference."""
     g = gen(51)
