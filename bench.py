@@ -158,16 +158,22 @@ def timed_replays(graph, replays: int) -> list[float]:
 
 
 def kernel_durations(work: Workload, calls: int, replays: int) -> dict:
-    """Per-kernel microseconds per call: a graph of ``calls`` back-to-back
-    launches of one kernel, rotating its buffer sets, replayed ``replays``
-    times.  Returns every replay's per-call average."""
-    out = {}
-    for name in KERNELS:
-        graph = capture(lambda: [work.launch(name, k) for k in range(calls)])
-        graph.replay()
+    """Per-kernel microseconds per call: one graph per kernel of ``calls``
+    back-to-back launches rotating its buffer sets; the graphs are replayed
+    round-robin ``replays`` times (after a warm-up) so clock or thermal drift
+    affects every kernel alike.  Returns every replay's per-call average."""
+    graphs = {name: capture(lambda name=name: [work.launch(name, k) for k in range(calls)])
+              for name in KERNELS}
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.5:  # bring clocks to their steady state
+        for graph in graphs.values():
+            graph.replay()
         torch.cuda.synchronize()
-        out[name] = [t / calls for t in timed_replays(graph, replays)]
-        del graph
+    out = {name: [] for name in KERNELS}
+    for _ in range(replays):
+        for name, graph in graphs.items():
+            out[name].append(timed_replays(graph, 1)[0] / calls)
+    del graphs
     return out
 
 
@@ -307,12 +313,37 @@ def cpu_baseline(reps: int = 3) -> dict:
             "cpu": platform.processor() or platform.machine(), "host_cpus": os.cpu_count()}
 
 
-def pmc_traffic() -> dict | None:
-    """HBM bytes per silu_mul launch from the committed rocprofv3 PMC summary."""
-    path = ROOT / "profiles" / "silu_mul_prefill_pmc.json"
-    if not path.exists():
+CALIBRATION_BYTES = 256 << 20  # one-way size of the --profile calibration copy
+PMC_SUMMARY = ROOT / "profiles" / "pmc_prefill_kernels.json"
+
+
+def pmc_traffic(kernel: str) -> float | None:
+    """HBM bytes per launch of ``kernel`` measured by rocprofv3 FETCH_SIZE and
+    WRITE_SIZE (committed summary, written from a ``--profile`` run)."""
+    if not PMC_SUMMARY.exists():
         return None
-    return json.loads(path.read_text())
+    entry = json.loads(PMC_SUMMARY.read_text()).get("kernels", {}).get(kernel)
+    return None if entry is None else entry["hbm_bytes_per_launch"]
+
+
+def profile_run(device, launches: int) -> None:
+    """Eager launches for counter collection: a calibration copy of known size
+    (CALIBRATION_BYTES read + written by torch's copy kernel), then each
+    prefill kernel ``launches`` times on rotating buffer sets."""
+    src = torch.empty(CALIBRATION_BYTES // 2, dtype=BF16, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    work = Workload(device)
+    torch.cuda.synchronize()
+    for name in KERNELS:
+        for k in range(launches):
+            work.launch(name, k)
+        torch.cuda.synchronize()
+    print(json.dumps({"profile": list(KERNELS), "launches": launches,
+                      "calibration_bytes": CALIBRATION_BYTES}), flush=True)
 
 
 def main() -> int:
@@ -322,6 +353,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode configs")
+    ap.add_argument("--profile", type=int, default=0, metavar="N",
+                    help="only run a calibration copy and N eager launches per prefill kernel "
+                         "(for rocprofv3 --pmc), then exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the fused kernels are per-row and need no "
@@ -333,6 +367,10 @@ def main() -> int:
         return 2
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.profile:
+        with torch.inference_mode():
+            profile_run(device, args.profile)
+        return 0
     print(f"bench: device {torch.cuda.get_device_name(device)}", file=sys.stderr, flush=True)
 
     with torch.inference_mode():
@@ -341,7 +379,7 @@ def main() -> int:
         work = Workload(device)
         torch.cuda.synchronize()
         print(f"bench: buffer sets {work.sets}", file=sys.stderr, flush=True)
-        durations = kernel_durations(work, calls=24, replays=max(5, args.steps // 24))
+        durations = kernel_durations(work, calls=24, replays=max(10, args.steps // 10))
         wall, gpu_seconds = run_prefill_step(work, args.steps, args.warmup)
         ms_per_step = wall * 1e3 / args.steps
         step_bytes = sum(BYTES.values())
@@ -369,11 +407,11 @@ def main() -> int:
                   flush=True)
 
     dominant = max(KERNELS, key=lambda n: kernels[n]["us_per_call_mean"])
-    traffic = pmc_traffic()
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": kernels[dominant]["gbps"],
                 "peak": PEAK_GBPS, "unit": "GB/s", "frac": kernels[dominant]["frac"],
-                "traffic": traffic["bytes_per_launch"] if traffic and traffic.get("kernel") == dominant else None,
-                "algorithmic_bytes": BYTES[dominant]}
+                "traffic": pmc_traffic(dominant), "algorithmic_bytes": BYTES[dominant]}
+    for name in KERNELS:
+        kernels[name]["hbm_bytes_pmc"] = pmc_traffic(name)
     result = {
         "metric": METRIC,
         "value": step_bytes / (ms_per_step * 1e6),

@@ -4,7 +4,7 @@
 // Embedding: out[i, :] = table[ids[i], :] - the nn.Embedding lookup of
 // engine/decode_step.py:38, engine/prefill.py:34, engine/decode.py:19.  One
 // wave copies one row with 16-byte loads and stores (lane i moves vectors i,
-// i+64, ...); the id is read once per wave.  Rows are copied as raw bits, so
+// i+64, ...); the id is read once per wave with a scalar load.  Rows are copied as raw bits, so
 // the result is bit-exact by construction.  Out-of-range ids give zero rows.
 //
 // Rotary table: the Qwen3 default RoPE table that engine/decode.py:52-59
@@ -16,6 +16,8 @@
 namespace qf {
 namespace {
 
+// NT: nontemporal stores for large calls (the gathered table rows are read
+// with ordinary cached loads - measured faster for this random-row pattern).
 template <int VPL, bool NT>
 __global__ __launch_bounds__(kBlock) void embedding_vec_kernel(const int64_t* __restrict__ ids,
                                                               const uint4* __restrict__ table,
@@ -23,8 +25,10 @@ __global__ __launch_bounds__(kBlock) void embedding_vec_kernel(const int64_t* __
                                                               int64_t n_ids, int64_t vocab,
                                                               int32_t nvec) {
   const int lane = threadIdx.x % kWave;
-  const int64_t row = (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
-  if (row >= n_ids) return;  // wave-uniform
+  // Wave-uniform row: the id is fetched with one scalar load.
+  const int64_t row = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) +
+                                                     threadIdx.x / kWave);
+  if (row >= n_ids) return;
   const int64_t id = ids[row];
   const bool valid = id >= 0 && id < vocab;
   const uint4* src = table + (valid ? id : 0) * nvec;
@@ -33,7 +37,7 @@ __global__ __launch_bounds__(kBlock) void embedding_vec_kernel(const int64_t* __
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int c = lane + k * kWave;
-    v[k] = (valid && c < nvec) ? load16<NT>(src + c) : make_uint4(0, 0, 0, 0);
+    v[k] = (valid && c < nvec) ? load16<false>(src + c) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {

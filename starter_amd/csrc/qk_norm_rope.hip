@@ -241,7 +241,7 @@ struct PrefillArgs {
 // to kUnitsPerWave consecutive units of one token: its loads all issue first,
 // the token's cos/sin row and both gains are unpacked once per wave, roles
 // are wave-uniform (scalar branches) and v units are pure copies.
-// Qwen3-4B: 6 units per token -> 3 waves.
+// Qwen3-4B: 6 units per token -> 3 waves of 2 units.
 constexpr int kUnitsPerWave = 2;
 constexpr int kRowLanes = 8;  // lanes per head row in the unit kernel
 
@@ -281,14 +281,14 @@ __device__ __forceinline__ void norm_rope16(const float* x, const float* w, cons
   hi = pack8(left + 8);
 }
 
-template <bool NT>
-__global__ __launch_bounds__(kBlock) void prefill_qkv_unit_kernel(PrefillArgs a) {
+template <bool NT, int UPW = kUnitsPerWave, int MIN_WAVES = 1>
+__global__ __launch_bounds__(kBlock, MIN_WAVES) void prefill_qkv_unit_kernel(PrefillArgs a) {
   const uint32_t wave =
       __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave);
   if (wave >= a.waves) return;  // wave-uniform
   const uint32_t token = __builtin_amdgcn_readfirstlane(fdiv(wave, a.waves_per_token));
   const uint32_t first =
-      __builtin_amdgcn_readfirstlane((wave - token * a.waves_per_token.d) * kUnitsPerWave);
+      __builtin_amdgcn_readfirstlane((wave - token * a.waves_per_token.d) * UPW);
   const uint32_t b = __builtin_amdgcn_readfirstlane(fdiv(token, a.length));
   const uint32_t t = token - b * a.length.d;
   const int lane = threadIdx.x % kWave;
@@ -297,9 +297,9 @@ __global__ __launch_bounds__(kBlock) void prefill_qkv_unit_kernel(PrefillArgs a)
 
   const int64_t width = (int64_t)a.heads.d * kD;
   const uint16_t* src = a.qkv + (int64_t)token * width + grp * kD + l * 8;
-  uint4 xlo[kUnitsPerWave], xhi[kUnitsPerWave];
+  uint4 xlo[UPW], xhi[UPW];
 #pragma unroll
-  for (int u = 0; u < kUnitsPerWave; ++u) {
+  for (int u = 0; u < UPW; ++u) {
     if (first + u < a.units) {
       const uint16_t* p = src + (int64_t)(first + u) * kRowLanes * kD;
       xlo[u] = load16<NT>(p);
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(kBlock) void prefill_qkv_unit_kernel(PrefillArgs a)
   unpack8(load16<false>(a.kw + l * 8 + kD / 2), wk + 8);
 
 #pragma unroll
-  for (int u = 0; u < kUnitsPerWave; ++u) {
+  for (int u = 0; u < UPW; ++u) {
     const uint32_t unit = first + u;
     if (unit >= a.units) break;  // wave-uniform
     uint16_t* dst;

@@ -43,73 +43,91 @@ __device__ __forceinline__ const uint16_t* row_base(const RmsArgs& a, int64_t r)
 }
 
 // Vector path: cols % 8 == 0 and every pointer / row stride 16-byte aligned.
-template <int LPR, int VPL, bool ADD, bool NT>
+// MODE: 0 = plain RMSNorm, 1 = add a bf16 branch, 2 = add f32 split-K partials.
+// A wave owns RPW rows (LPR == 64) and issues all of their loads before any
+// arithmetic; NT selects nontemporal row loads / stores for large calls.
+template <int LPR, int VPL, int MODE, int RPW, bool NT>
 __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
-  constexpr int kRowsPerBlock = kBlock / LPR;
+  constexpr bool ADD = MODE != 0;
+  constexpr int kRowsPerBlock = kBlock / LPR * RPW;
   const int lane = threadIdx.x % LPR;
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / LPR;
-  const bool live = row < a.rows;
-  const int64_t r = live ? row : 0;
+  const int64_t row0 = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x / LPR) * RPW;
 
-  const uint4* xin = reinterpret_cast<const uint4*>(row_base<ADD>(a, r));
-  float t[VPL][8];
-  double ss = 0.0;
-
+  uint4 xv[RPW][VPL], bv[RPW][VPL];
 #pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int v = lane + k * LPR;
-    const bool on = live && v < a.nvec;
-    uint4 xv = on ? load16<NT>(xin + v) : make_uint4(0, 0, 0, 0);
-    unpack8(xv, t[k]);
-    if constexpr (ADD) {
-      float y[8];
-      if (a.splits == 0) {
-        const uint4* b = reinterpret_cast<const uint4*>(
-            static_cast<const uint16_t*>(a.branch) + r * a.cols);
-        uint4 bv = on ? load16<NT>(b + v) : make_uint4(0, 0, 0, 0);
-        unpack8(bv, y);
-      } else {
-        // f32 partials: two 16-byte halves per 8 columns, summed in split order.
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t row = row0 + r;
+    const bool live = row < a.rows;
+    const uint4* xin = reinterpret_cast<const uint4*>(row_base<ADD>(a, live ? row : 0));
+    const uint4* bin = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.branch) +
+                                                      (live ? row : 0) * a.cols);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = 0.0f;
-        const float* p = static_cast<const float*>(a.branch) + r * a.cols + (int64_t)v * 8;
-        for (int s = 0; s < a.splits; ++s) {
-          const uint4 p0 = on ? load16<NT>(p) : make_uint4(0, 0, 0, 0);
-          const uint4 p1 = on ? load16<NT>(p + 4) : make_uint4(0, 0, 0, 0);
-          y[0] += __uint_as_float(p0.x); y[1] += __uint_as_float(p0.y);
-          y[2] += __uint_as_float(p0.z); y[3] += __uint_as_float(p0.w);
-          y[4] += __uint_as_float(p1.x); y[5] += __uint_as_float(p1.y);
-          y[6] += __uint_as_float(p1.z); y[7] += __uint_as_float(p1.w);
-          p += a.split_stride;
-        }
-        round8(y);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) t[k][j] += y[j];
-      uint4 tv = pack8(t[k]);
-      unpack8(tv, t[k]);
-      if (on) store16<NT>(reinterpret_cast<uint4*>(a.total + row * a.cols) + v, tv);
+    for (int k = 0; k < VPL; ++k) {
+      const int v = lane + k * LPR;
+      const bool on = live && v < a.nvec;
+      xv[r][k] = on ? load16<NT>(xin + v) : make_uint4(0, 0, 0, 0);
+      if constexpr (MODE == 1) bv[r][k] = on ? load16<NT>(bin + v) : make_uint4(0, 0, 0, 0);
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ss += (double)(t[k][j] * t[k][j]);
   }
 
-  const float inv = inv_rms(group_sum_f64<LPR>(ss), (float)a.cols, a.eps);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t row = row0 + r;
+    const bool live = row < a.rows;
+    const int64_t rr = live ? row : 0;
+    float t[VPL][8];
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int v = lane + k * LPR;
+      const bool on = live && v < a.nvec;
+      unpack8(xv[r][k], t[k]);
+      if constexpr (ADD) {
+        float y[8];
+        if constexpr (MODE == 1) {
+          unpack8(bv[r][k], y);
+        } else {
+          // f32 partials: two 16-byte halves per 8 columns, summed in split order.
+#pragma unroll
+          for (int j = 0; j < 8; ++j) y[j] = 0.0f;
+          const float* p = static_cast<const float*>(a.branch) + rr * a.cols + (int64_t)v * 8;
+          for (int s = 0; s < a.splits; ++s) {
+            const uint4 p0 = on ? load16<NT>(p) : make_uint4(0, 0, 0, 0);
+            const uint4 p1 = on ? load16<NT>(p + 4) : make_uint4(0, 0, 0, 0);
+            y[0] += __uint_as_float(p0.x); y[1] += __uint_as_float(p0.y);
+            y[2] += __uint_as_float(p0.z); y[3] += __uint_as_float(p0.w);
+            y[4] += __uint_as_float(p1.x); y[5] += __uint_as_float(p1.y);
+            y[6] += __uint_as_float(p1.z); y[7] += __uint_as_float(p1.w);
+            p += a.split_stride;
+          }
+          round8(y);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[k][j] += y[j];
+        const uint4 tv = pack8(t[k]);
+        unpack8(tv, t[k]);
+        if (on) store16<NT>(reinterpret_cast<uint4*>(a.total + rr * a.cols) + v, tv);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += (double)(t[k][j] * t[k][j]);
+    }
 
-  const uint4* wv = reinterpret_cast<const uint4*>(a.w);
-  uint4* o = reinterpret_cast<uint4*>(a.out + r * a.cols);
+    const float inv = inv_rms(group_sum_f64<LPR>(ss), (float)a.cols, a.eps);
+    const uint4* wv = reinterpret_cast<const uint4*>(a.w);
+    uint4* o = reinterpret_cast<uint4*>(a.out + rr * a.cols);
 #pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int v = lane + k * LPR;
-    const bool on = live && v < a.nvec;
-    float n[8], w[8];
+    for (int k = 0; k < VPL; ++k) {
+      const int v = lane + k * LPR;
+      const bool on = live && v < a.nvec;
+      float n[8], w[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) n[j] = t[k][j] * inv;
-    round8(n);
-    unpack8(on ? wv[v] : make_uint4(0, 0, 0, 0), w);
+      for (int j = 0; j < 8; ++j) n[j] = t[k][j] * inv;
+      round8(n);
+      unpack8(on ? wv[v] : make_uint4(0, 0, 0, 0), w);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) n[j] *= w[j];
-    if (on) store16<NT>(o + v, pack8(n));
+      for (int j = 0; j < 8; ++j) n[j] *= w[j];
+      if (on) store16<NT>(o + v, pack8(n));
+    }
   }
 }
 
@@ -155,48 +173,52 @@ __global__ __launch_bounds__(kBlock) void rms_scalar_kernel(RmsArgs a) {
   }
 }
 
-template <int LPR, int VPL, bool ADD>
-int launch_vec(const RmsArgs& a, hipStream_t s) {
-  const int64_t blocks = (a.rows + (kBlock / LPR) - 1) / (kBlock / LPR);
-  const int64_t bytes = a.rows * a.cols * 2 * (ADD ? 4 : 2);
-  if (bytes >= kStreamBytes)
-    hipLaunchKernelGGL((rms_vec_kernel<LPR, VPL, ADD, true>), dim3((unsigned)blocks), dim3(kBlock),
-                       0, s, a);
-  else
-    hipLaunchKernelGGL((rms_vec_kernel<LPR, VPL, ADD, false>), dim3((unsigned)blocks), dim3(kBlock),
-                       0, s, a);
+template <int LPR, int VPL, int MODE, int RPW, bool NT>
+int launch_rows(const RmsArgs& a, hipStream_t s) {
+  constexpr int64_t per_block = kBlock / LPR * RPW;
+  const int64_t blocks = (a.rows + per_block - 1) / per_block;
+  hipLaunchKernelGGL((rms_vec_kernel<LPR, VPL, MODE, RPW, NT>), dim3((unsigned)blocks), dim3(kBlock),
+                     0, s, a);
   return launch_status();
 }
 
-template <bool ADD>
+// Large calls stream with nontemporal accesses and, for rows of at most five
+// vectors per lane (<= 2560 columns) with a bf16 or no branch, two rows per
+// wave; decode-size calls keep one row per wave and cached accesses.
+template <int LPR, int VPL, int MODE>
+int launch_vec(const RmsArgs& a, hipStream_t s) {
+  const int64_t bytes = a.rows * a.cols * 2 * (MODE == 0 ? 2 : 4);
+  if (bytes < kStreamBytes) return launch_rows<LPR, VPL, MODE, 1, false>(a, s);
+  if constexpr (LPR == 64 && VPL <= 5 && MODE != 2) return launch_rows<LPR, VPL, MODE, 2, true>(a, s);
+  return launch_rows<LPR, VPL, MODE, 1, true>(a, s);
+}
+
+template <int MODE>
 int dispatch(RmsArgs a, bool vec_ok, hipStream_t s) {
+  constexpr bool ADD = MODE != 0;
   if (a.rows == 0) return QF_OK;
-  if (!vec_ok) {
-    const int64_t blocks = (a.rows + 3) / 4;
-    hipLaunchKernelGGL((rms_scalar_kernel<ADD>), dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
-    return launch_status();
+  if (vec_ok) {
+    a.nvec = (int32_t)(a.cols / 8);
+    const int nv = a.nvec;
+    if (nv <= 8) return launch_vec<8, 1, MODE>(a, s);
+    if (nv <= 16) return launch_vec<16, 1, MODE>(a, s);
+    if (nv <= 32) return launch_vec<32, 1, MODE>(a, s);
+    switch ((nv + 63) / 64) {
+      case 1: return launch_vec<64, 1, MODE>(a, s);
+      case 2: return launch_vec<64, 2, MODE>(a, s);
+      case 3: return launch_vec<64, 3, MODE>(a, s);
+      case 4: return launch_vec<64, 4, MODE>(a, s);
+      case 5: return launch_vec<64, 5, MODE>(a, s);
+      case 6: return launch_vec<64, 6, MODE>(a, s);
+      case 7: return launch_vec<64, 7, MODE>(a, s);
+      case 8: return launch_vec<64, 8, MODE>(a, s);
+      case 9: case 10: return launch_vec<64, 10, MODE>(a, s);
+      case 11: case 12: return launch_vec<64, 12, MODE>(a, s);
+      case 13: case 14: return launch_vec<64, 14, MODE>(a, s);
+      case 15: case 16: return launch_vec<64, 16, MODE>(a, s);
+      default: break;  // wider than 8192 columns: the scalar path handles any width
+    }
   }
-  a.nvec = (int32_t)(a.cols / 8);
-  const int nv = a.nvec;
-  if (nv <= 8) return launch_vec<8, 1, ADD>(a, s);
-  if (nv <= 16) return launch_vec<16, 1, ADD>(a, s);
-  if (nv <= 32) return launch_vec<32, 1, ADD>(a, s);
-  switch ((nv + 63) / 64) {
-    case 1: return launch_vec<64, 1, ADD>(a, s);
-    case 2: return launch_vec<64, 2, ADD>(a, s);
-    case 3: return launch_vec<64, 3, ADD>(a, s);
-    case 4: return launch_vec<64, 4, ADD>(a, s);
-    case 5: return launch_vec<64, 5, ADD>(a, s);
-    case 6: return launch_vec<64, 6, ADD>(a, s);
-    case 7: return launch_vec<64, 7, ADD>(a, s);
-    case 8: return launch_vec<64, 8, ADD>(a, s);
-    case 9: case 10: return launch_vec<64, 10, ADD>(a, s);
-    case 11: case 12: return launch_vec<64, 12, ADD>(a, s);
-    case 13: case 14: return launch_vec<64, 14, ADD>(a, s);
-    case 15: case 16: return launch_vec<64, 16, ADD>(a, s);
-    default: break;
-  }
-  // Wider than 8192 columns: the scalar path handles any width.
   const int64_t blocks = (a.rows + 3) / 4;
   hipLaunchKernelGGL((rms_scalar_kernel<ADD>), dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
   return launch_status();
@@ -226,7 +248,7 @@ extern "C" int qf_rms_norm(const void* x, int64_t rows, int64_t cols, int64_t in
   a.eps = eps;
   const bool vec_ok = cols % 8 == 0 && outer_stride % 8 == 0 && inner_stride % 8 == 0 &&
                       aligned16(x) && aligned16(weight) && aligned16(out);
-  return dispatch<false>(a, vec_ok, as_stream(stream));
+  return dispatch<0>(a, vec_ok, as_stream(stream));
 }
 
 extern "C" int qf_add_rms_norm(const void* residual, const void* branch, int32_t splits,
@@ -250,5 +272,6 @@ extern "C" int qf_add_rms_norm(const void* residual, const void* branch, int32_t
   a.eps = eps;
   const bool vec_ok = cols % 8 == 0 && aligned16(residual) && aligned16(branch) &&
                       aligned16(weight) && aligned16(total) && aligned16(normed);
-  return dispatch<true>(a, vec_ok, as_stream(stream));
+  return splits == 0 ? dispatch<1>(a, vec_ok, as_stream(stream))
+                     : dispatch<2>(a, vec_ok, as_stream(stream));
 }
