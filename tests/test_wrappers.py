@@ -286,3 +286,15 @@ def test_fused_embedding_shares_the_weight_parameter():
     assert fused.weight is ref.weight
     with pytest.raises(ValueError):
         embedding.FusedEmbedding(torch.nn.Embedding(10, 8, max_norm=1.0))
+
+
+def test_skinny_gemm_stand_in_declines_every_shape():
+    """engine/decode_step.py:22-30 falls back to F.linear when supports() is False."""
+    from starter_amd.kernels import skinny_gemm
+    x, w = Fake((4, 2560)), Fake((6144, 2560))
+    assert skinny_gemm.supports(x, w) is False
+    assert skinny_gemm.supports(x, Fake((19456, 2560)), pairs=True) is False
+    with pytest.raises(ValueError):
+        skinny_gemm.linear_partials(x, w)
+    with pytest.raises(ValueError):
+        skinny_gemm.linear_silu_mul(x, w)
