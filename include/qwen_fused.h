@@ -2,7 +2,8 @@
  * qwen_fused.h - C ABI of the MI355X (gfx950) fused layer kernels of the
  * Qwen3-4B decode engine: residual-add + RMSNorm, per-head Q/K RMSNorm fused
  * with NeoX rotary embedding (three layouts), SiLU(gate)*up, the token
- * embedding gather and the rotary cos/sin table builder.
+ * embedding gather, the rotary cos/sin table builder, and the split-K decode
+ * projections that feed the fused consumers.
  *
  * Conventions shared by every entry point:
  *   - Tensors are plain device pointers.  "bf16" buffers hold IEEE bfloat16
@@ -155,6 +156,45 @@ int qf_embedding(const int64_t* ids, int64_t n_ids, const void* table,
 int qf_rope_table(const float* inv_freq, int32_t half, const int64_t* positions,
                   int64_t start, int64_t n_pos, void* cos, void* sin,
                   void* stream);
+
+/*
+ * Decode projections for at most 64 rows (the shape rule of
+ * engine/kernels/skinny_gemm.py:75-83 supports()): x bf16 [rows, k] and
+ * W bf16 [n, k], both contiguous; 1 <= rows <= 64, k % 64 == 0, n % 32 == 0;
+ * x, W and partials 16-byte aligned.  Otherwise QF_E_SHAPE / QF_E_ALIGN.
+ *
+ * qf_linear_splits: the number of K splits qf_linear_partials is meant to be
+ * called with for this shape (>= 1, a power of two dividing k / 64), or a
+ * negative status.  Replaces split_count (engine/kernels/skinny_gemm.py:86-91);
+ * unlike the reference's it also depends on rows.
+ */
+int qf_linear_splits(int64_t rows, int64_t k, int64_t n);
+
+/*
+ * f32 split-K partials of y = x @ W^T:
+ *   partials[s, m, j] = sum over c in [s*k/splits, (s+1)*k/splits) of
+ *                       float(x[m, c]) * float(W[j, c])
+ * accumulated in f32 (products exact; addition order fixed by the matrix
+ * cores, deterministic).  partials is contiguous f32 [splits, rows, n];
+ * splits >= 1 must divide k / 64 (QF_E_ARG otherwise).  qf_add_rms_norm and
+ * qf_qkv_norm_rope_cache take the result directly.
+ * Replaces linear_partials + _partials_kernel (engine/kernels/skinny_gemm.py:
+ * 28-46, 100-109).
+ */
+int qf_linear_partials(const void* x, int64_t rows, int64_t k, const void* weight,
+                       int64_t n, int32_t splits, void* partials, void* stream);
+
+/*
+ * Decode gate/up projection with the SiLU * up epilogue, for a packed
+ * weight gate_up bf16 [2n, k] (gate rows first):
+ *   g = bf16(x @ gate^T),  u = bf16(x @ up^T)     (f32 accumulation, as above)
+ *   out[m, j] = bf16(float(bf16(silu(g))) * float(u)),  silu(g) = g / (1 + exp(-g))
+ * out is contiguous bf16 [rows, n], 8-byte aligned.
+ * Replaces linear_silu_mul + _silu_mul_kernel (engine/kernels/skinny_gemm.py:
+ * 49-72, 112-121).
+ */
+int qf_linear_silu_mul(const void* x, int64_t rows, int64_t k, const void* gate_up,
+                       int64_t n, void* out, void* stream);
 
 #ifdef __cplusplus
 }

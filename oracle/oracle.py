@@ -37,6 +37,8 @@ _SIGNATURES = {
                         _vp, _vp, _vp], None),
     "or_embedding": ([_vp, _i64, _vp, _i64, _i64, _vp], None),
     "or_rope_table": ([_vp, _i32, _vp, _i64, _i64, _vp, _vp], None),
+    "or_linear_partials": ([_vp, _i64, _i64, _vp, _i64, _i32, _vp], None),
+    "or_linear_silu_mul": ([_vp, _i64, _i64, _vp, _i64, _vp], None),
 }
 
 
@@ -219,3 +221,29 @@ def default_inv_freq(theta: float, dim: int) -> np.ndarray:
 
 
 __all__ = [name for name in dir() if not name.startswith("_") and name not in ("annotations", "ctypes", "np", "Path")]
+
+
+def linear_partials(x, weight, splits: int) -> np.ndarray:
+    """engine/kernels/skinny_gemm.py:28-46, 100-109: f32 [splits, M, N] partials of
+    x [M, K] @ weight [N, K].T over K/splits-wide chunks (exactly rounded)."""
+    x, weight = _u16(x), _u16(weight)
+    m, k = x.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k or splits < 1 or k % splits:
+        raise ValueError("linear_partials: shapes disagree")
+    out = np.empty((splits, m, n), dtype=np.float32)
+    lib().or_linear_partials(_p(x), m, k, _p(weight), n, splits, _p(out))
+    return out
+
+
+def linear_silu_mul(x, gate_up) -> np.ndarray:
+    """engine/kernels/skinny_gemm.py:49-72, 112-121: bf16 bits [M, N] of
+    silu(bf16(x @ gate.T)) * bf16(x @ up.T) for a packed [2N, K] weight."""
+    x, gate_up = _u16(x), _u16(gate_up)
+    m, k = x.shape
+    width = gate_up.shape[0]
+    if gate_up.shape[1] != k or width % 2:
+        raise ValueError("linear_silu_mul: shapes disagree")
+    out = np.empty((m, width // 2), dtype=np.uint16)
+    lib().or_linear_silu_mul(_p(x), m, k, _p(gate_up), width // 2, _p(out))
+    return out

@@ -33,6 +33,14 @@
  *                          change bits.
  *   or_embedding           F.embedding on CPU, bit-exact.
  *   or_rope_table          Qwen3RotaryEmbedding.forward on CPU, <= 1 bf16 ulp.
+ *   or_linear_partials     integer inputs against an int64 matmul, bit-exact
+ *                          per split; torch float64 F.linear per chunk;
+ *                          dropped-chunk and transposed-operand mistakes
+ *                          must be detected.
+ *   or_linear_silu_mul     composition of exactly rounded projections with
+ *                          or_silu_mul (bit-exact), torch float64 projections
+ *                          + F.silu; skipping the projection rounding must
+ *                          change bits (the reference's negative control).
  */
 #include <math.h>
 #include <stdint.h>
@@ -311,4 +319,45 @@ EXPORT void or_rope_table(const float* inv_freq, int32_t half, const int64_t* po
       sin_out[p * 2 * half + j + half] = s;
     }
   }
+}
+
+/* ---------------------------------------------------- decode projections */
+
+/* Exactly rounded f32 value of sum_c x[c] * w[c] over [c0, c1): the bf16
+ * products are exact in double and so is their sum up to a relative 2^-40
+ * for any realistic length, so rounding the double sum once to f32 gives
+ * the correctly rounded dot product.  A hardware f32 accumulation (tensor or
+ * matrix cores) differs from it by f32 rounding error only. */
+static float dot_f32(const uint16_t* x, const uint16_t* w, int64_t c0, int64_t c1) {
+  double acc = 0.0;
+  for (int64_t c = c0; c < c1; ++c) acc += (double)or_f32(x[c]) * (double)or_f32(w[c]);
+  return (float)acc;
+}
+
+/* engine/kernels/skinny_gemm.py:28-46 (_partials_kernel) and :100-109:
+ * partial s of x @ W^T over k in [s*k/S, (s+1)*k/S) with f32 accumulation
+ * (tl.dot on bf16 operands).  x is [m, k], W is [n, k], out is f32
+ * [splits, m, n]. */
+EXPORT void or_linear_partials(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w,
+                               int64_t n, int32_t splits, float* out) {
+  const int64_t per = k / splits;
+  for (int32_t s = 0; s < splits; ++s)
+    for (int64_t i = 0; i < m; ++i)
+      for (int64_t j = 0; j < n; ++j)
+        out[((int64_t)s * m + i) * n + j] = dot_f32(x + i * k, w + j * k, s * per, (s + 1) * per);
+}
+
+/* engine/kernels/skinny_gemm.py:49-72 (_silu_mul_kernel) and :112-121:
+ *   g = bf16(x @ gate^T), u = bf16(x @ up^T)     (each projection a bf16 tensor)
+ *   out = bf16(bf16(g / (1 + exp(-g))) * u)      (as or_silu_mul)
+ * gate_up is the packed [2n, k] weight, gate rows first; out is [m, n]. */
+EXPORT void or_linear_silu_mul(const uint16_t* x, int64_t m, int64_t k, const uint16_t* gate_up,
+                               int64_t n, uint16_t* out) {
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) {
+      const float g = rbf(dot_f32(x + i * k, gate_up + j * k, 0, k));
+      const float u = rbf(dot_f32(x + i * k, gate_up + (n + j) * k, 0, k));
+      const float act = rbf(g / (1.0f + expf(-g)));
+      out[i * n + j] = or_bf16(act * u);
+    }
 }

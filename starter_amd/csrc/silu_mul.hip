@@ -4,47 +4,22 @@
 // tensors in engine/mlp.py:19-21):
 //   a   = bf16(g / (1 + exp(-g)))
 //   out = bf16(float(a) * float(u))
-// The f32 SiLU is first evaluated cheaply: exp(-g) = 2^t on the hardware exp2
-// (v_exp_f32) with t = -g * log2 e, the rounding error of t restored by one
-// FMA (2^(t + dt) ~= 2^t * (1 + dt ln 2)), and g / d as g * (1 / d) on the
-// hardware reciprocal (v_rcp_f32).  That value is within a few f32 ulps of the
-// correctly rounded quotient; it can only round to a different bf16 when it
-// lies near a bf16 rounding midpoint, so an element within kBand f32 ulps of
-// one - or whose reciprocal would be denormal (g < -86.6) - is recomputed
-// with the f32 formula itself (expf, IEEE divide).  That happens for ~0.05%
-// of elements.  bf16(silu(g)) depends only on the 16-bit gate, and the tests
-// check every one of the 65,536 gate values against the oracle bit for bit.
-// The cheap path costs ~9 VALU instructions per element instead of ~25 for
-// expf and an IEEE divide, which would make the kernel VALU-bound.
+// The f32 SiLU is silu_f32 (qf_silu.h): hardware exp2 and reciprocal with an
+// exact fallback near bf16 rounding midpoints, so bf16(silu) matches the f32
+// formula for every bf16 gate; the tests check all 65,536 gate values against
+// the oracle bit for bit.  The cheap path costs ~9 VALU instructions per
+// element instead of ~25 for expf and an IEEE divide, which would make the
+// kernel VALU-bound.
 //
 // Layout: the output is a flat sequence of 16-byte vectors (8 columns).  A
 // thread owns U vectors spaced one workgroup apart, so each wave-wide access
 // covers 1 KiB of consecutive gate, up or output bytes.  Row / column of a
 // vector come from a multiply-high division by the per-row vector count.
 #include "qf_device.h"
+#include "qf_silu.h"
 
 namespace qf {
 namespace {
-
-constexpr float kLog2e = 0x1.715476p+0f;     // log2(e) rounded to f32
-constexpr float kLog2eLo = 0x1.4ae0c0p-26f;  // log2(e) - kLog2e
-constexpr float kLn2 = 0x1.62e430p-1f;
-constexpr int kBand = 16;                    // f32 ulps around a bf16 midpoint
-
-// g / (1 + exp(-g)) with every step correctly rounded in f32.
-__device__ __attribute__((noinline)) float silu_exact(float g) { return g / (1.0f + expf(-g)); }
-
-__device__ __forceinline__ float silu_f32(float g) {
-  const float t = -g * kLog2e;
-  const float dt = __builtin_fmaf(-g, kLog2e, -t) + (-g) * kLog2eLo;  // t's rounding error
-  const float e0 = __builtin_amdgcn_exp2f(t);                         // v_exp_f32
-  const float e = __builtin_fmaf(e0, dt * kLn2, e0);
-  const float d = 1.0f + e;
-  const float a = g * __builtin_amdgcn_rcpf(d);                       // v_rcp_f32
-  const int low = (int)(__float_as_uint(a) & 0xffffu);                // bits below bf16
-  if (__builtin_expect(abs(low - 0x8000) < kBand || !(d < 0x1p125f), 0)) return silu_exact(g);
-  return a;
-}
 
 __device__ __forceinline__ uint4 silu_mul8(const uint4& gv, const uint4& uv) {
   float g[8], u[8];

@@ -1,0 +1,401 @@
+// Decode projections y = x @ W^T for at most 64 rows of x, on the gfx950
+// matrix cores (engine/kernels/skinny_gemm.py:28-121 is the reference:
+// _partials_kernel :28-46, _silu_mul_kernel :49-72).
+//
+// A decode step multiplies a few rows by every layer weight, so each call is
+// a weight stream: W ([N, K] bf16, K contiguous) is read once from HBM and x
+// (at most 64 x K bf16) comes from L2.  The arithmetic is small next to the
+// bytes (2*M flops per weight byte), but at M = 64 it is beyond what the VALU
+// does at HBM speed, so every product runs on v_mfma_f32_16x16x32_bf16:
+//
+//   A operand = 16 rows of W (one n-tile), B operand = 16 rows of x (one
+//   m-tile), 32 k per instruction.  Lane l holds A row (l % 16) and B column
+//   (l % 16), k = 8*(l / 16) .. +8 of the step.  The f32 result lane l holds
+//   is D[4*(l/16) + i][l % 16] = y[m0 + l%16][n0 + 4*(l/16) + i]: four
+//   consecutive output columns of one x row, one 16-byte store.
+//
+// Loading W straight into that layout would make every 16 lanes of a load
+// touch 16 different rows; HBM streams far better when each row is read a
+// whole 128-byte line at a time.  So W moves in 64-wide k chunks: one
+// 16-byte load per lane reads 8 rows x 128 contiguous bytes (two loads per
+// 16-row tile), the wave writes the chunk to its own LDS staging tile (row
+// stride padded to 144 bytes, conflict-free both ways) and reads it back in
+// MFMA layout.  Only the wave itself touches its staging tile, so no
+// workgroup barrier is needed in the loop.  Each wave keeps D chunks of loads
+// in flight (software pipelined).
+//
+// A workgroup owns NT n-tiles and one K range (its split); its four waves
+// take interleaved chunks of that range, so together they read consecutive
+// bytes of every row, and reduce their f32 tiles through LDS in wave order.
+// Rows of x beyond M are never stored.
+//
+// Two epilogues, as in the reference:
+//   * qf_linear_partials: the workgroup's f32 tile is split `split`'s partial
+//     [S, M, N]; the consumers (qf_add_rms_norm, qf_qkv_norm_rope_cache) add
+//     the S partials in order and round once to bf16.  No atomics, no extra
+//     reduction launch.
+//   * qf_linear_silu_mul: the workgroup owns gate rows [c, c+16h) and the
+//     matching up rows [N + c, ...) of the packed [2N, K] weight over all of
+//     K, and writes bf16(bf16(silu(bf16(gate))) * bf16(up)).
+//
+// Numerics: bf16 x bf16 products are exact in f32; the MFMA adds them in f32
+// in an order fixed by the hardware, and the wave hand-off adds the four
+// waves' sums in wave order.  Results are deterministic run to run; they
+// equal the exactly rounded dot product whenever every partial sum is an
+// exactly representable f32 (e.g. integer inputs below 2^24), and otherwise
+// differ from it by f32 accumulation error only.
+#include "qf_device.h"
+#include "qf_silu.h"
+
+namespace qf {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 16;    // rows of W (output columns) per n-tile; rows of x per m-tile
+constexpr int kStep = 32;    // k per MFMA
+constexpr int kChunk = 64;   // k per wave chunk; the shape rule's k granularity
+constexpr int kWaves = kBlock / kWave;
+constexpr int kMaxRows = 64;
+constexpr int kColAlign = 32;  // N granularity of the shape rule
+
+struct SkinnyArgs {
+  const uint16_t* x;   // [m, k]
+  const uint16_t* w;   // [n, k], or [2n, k] gate rows then up rows
+  float* partials;     // [splits, m, n]
+  uint16_t* out;       // [m, n]
+  int64_t k;
+  int32_t m;
+  int32_t n;           // output columns
+  int32_t chunks;      // 64-wide k chunks per split
+};
+
+__device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Orders one wave's LDS writes before its reads of other lanes' data (and the
+// reads before the next writes); LDS executes a wave's operations in order,
+// so this costs no instruction.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+constexpr int kLdsRow = kChunk * 2 + 16;       // padded staging row: 144 bytes
+constexpr int kTileLds = kTile * kLdsRow;      // one 16-row staging tile
+constexpr int kRowsPerLoad = kWave * 16 / (kChunk * 2);  // 8 rows x 128 B per load
+
+// MT m-tiles of x (M <= 16*MT); NT n-tiles of W per wave (for PAIRS the
+// first NT/2 are gate tiles, the rest the matching up tiles); the four waves
+// form WN = 4/WK groups of distinct n-tiles, each group WK waves that split
+// the chunks; D chunks in flight per wave; NTL = nontemporal weight loads.
+// Waves of different groups read the same x chunk at about the same time,
+// so x is fetched from L2 once per workgroup rather than once per wave.
+template <int MT, int NT, int WK, int D, bool PAIRS, bool NTL, bool XT>
+__global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
+  static_assert(kWaves % WK == 0, "wave split");
+  constexpr int WN = kWaves / WK;
+  constexpr int kCols = PAIRS ? NT / 2 : NT;  // output n-tiles per wave
+  constexpr int kStageTiles = NT + (XT ? MT : 0);
+  constexpr int kStageBytes = kWaves * kStageTiles * kTileLds;
+  constexpr int kHandoffBytes = WN * (WK - 1) * NT * MT * kWave * 16;
+  __shared__ __attribute__((aligned(16)))
+      uint8_t lds[kStageBytes > kHandoffBytes ? kStageBytes : kHandoffBytes];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int r = lane % kTile;
+  const int g = lane / kTile;
+  const int wk = wave % WK;  // position among the waves sharing n-tiles
+  const int wn = wave / WK;  // n-tile group
+  const int col0 = (blockIdx.x * WN + wn) * (kTile * kCols);
+  const bool live = col0 < a.n;  // the last workgroup's groups may lie past N
+  const int split = blockIdx.y;
+  const int64_t kbase = (int64_t)split * a.chunks * kChunk;
+
+  // Chunk loads: lane reads row (lane / 8) + 8*i of the tile, 16 bytes at
+  // column 8 * (lane % 8) of the chunk.
+  const uint16_t* wp[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    int row = col0 + kTile * t;
+    if (PAIRS && t >= kCols) row = a.n + col0 + kTile * (t - kCols);
+    wp[t] = a.w + (int64_t)(row + lane / 8) * a.k + kbase + 8 * (lane % 8);
+  }
+  const int64_t wstep = (int64_t)kRowsPerLoad * a.k;
+  // Lanes of x rows beyond M read row 0 instead: the MFMA keeps every
+  // output column separate, and those columns are never stored.
+  const uint16_t* xp[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if constexpr (XT) {  // coalesced like W, transposed through LDS
+        const int row = kTile * mt + kRowsPerLoad * i + lane / 8;
+        xp[mt][i] = a.x + (int64_t)(row < a.m ? row : 0) * a.k + kbase + 8 * (lane % 8);
+      } else {             // straight into MFMA layout
+        const int row = kTile * mt + r;
+        xp[mt][i] = a.x + (int64_t)(row < a.m ? row : 0) * a.k + kbase + 8 * g + kStep * i;
+      }
+    }
+  uint8_t* stage = lds + wave * kStageTiles * kTileLds;
+  const int wr_off = (lane / 8) * kLdsRow + 16 * (lane % 8);
+  const int rd_off = r * kLdsRow + 16 * g;
+
+  f32x4 acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  uint4 wv[D][NT][2], xv[D][MT][2];
+  // This wave's chunks are wk, wk + WK, ...: n_own of them.
+  const int n_own = live && a.chunks > wk ? (a.chunks - wk + WK - 1) / WK : 0;
+
+  auto issue = [&](int d, int j) {
+    const int64_t off = (int64_t)(wk + WK * j) * kChunk;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) wv[d][t][i] = load16<NTL>(wp[t] + off + i * wstep);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) xv[d][mt][i] = load16<false>(xp[mt][i] + off);
+  };
+  auto consume = [&](int d) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        *reinterpret_cast<uint4*>(stage + t * kTileLds + wr_off + i * kRowsPerLoad * kLdsRow) =
+            wv[d][t][i];
+    if constexpr (XT) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          *reinterpret_cast<uint4*>(stage + (NT + mt) * kTileLds + wr_off + i * kRowsPerLoad * kLdsRow) =
+              xv[d][mt][i];
+    }
+    wave_lds_fence();
+    uint4 fw[NT][2], fx[MT][2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        fw[t][s] = *reinterpret_cast<const uint4*>(stage + t * kTileLds + rd_off + s * kStep * 2);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        fx[mt][s] = XT ? *reinterpret_cast<const uint4*>(stage + (NT + mt) * kTileLds + rd_off + s * kStep * 2)
+                       : xv[d][mt][s];
+    }
+    wave_lds_fence();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma(fw[t][s], fx[mt][s], acc[t][mt]);
+  };
+
+  // Software pipeline with D chunks in flight.  The steady-state loop issues
+  // unconditionally, so the compiler's wait counts stay exact (each consume
+  // waits only for its own chunk); only the last 2*D chunks take branches.
+  if (n_own >= D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, d);
+    int j = 0;
+    for (; j + 2 * D <= n_own; j += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        consume(d);
+        issue(d, j + d + D);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      consume(d);
+      if (j + d + D < n_own) issue(d, j + d + D);
+    }
+    j += D;
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (j + d < n_own) consume(d);
+  } else {
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d < n_own) issue(d, d);
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d < n_own) consume(d);
+  }
+
+  // Waves wk = 1..WK-1 of each group hand their tiles to the group's wave
+  // wk = 0, which adds them in wave order.
+  if constexpr (WK > 1) {
+    __syncthreads();
+    f32x4* handoff = reinterpret_cast<f32x4*>(lds);
+    constexpr int kPer = NT * MT * kWave;
+    if (wk > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          handoff[(wn * (WK - 1) + wk - 1) * kPer + (t * MT + mt) * kWave + lane] = acc[t][mt];
+    }
+    __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int w = 0; w < WK - 1; ++w)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[t][mt] += handoff[(wn * (WK - 1) + w) * kPer + (t * MT + mt) * kWave + lane];
+  }
+
+  if (!live) return;
+  if constexpr (!PAIRS) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = kTile * mt + r;
+      if (m >= a.m) continue;
+      float* dst = a.partials + ((int64_t)split * a.m + m) * a.n + col0 + 4 * g;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) *reinterpret_cast<f32x4*>(dst + kTile * t) = acc[t][mt];
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = kTile * mt + r;
+      if (m >= a.m) continue;
+      uint16_t* dst = a.out + (int64_t)m * a.n + col0 + 4 * g;
+#pragma unroll
+      for (int h = 0; h < kCols; ++h) {
+        float y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // Each projection is a bf16 tensor in the reference; SiLU is
+          // rounded to bf16 before the bf16 product.
+          const float gate = from_bf16(to_bf16(acc[h][mt][i]));
+          const float up = from_bf16(to_bf16(acc[kCols + h][mt][i]));
+          y[i] = from_bf16(to_bf16(silu_f32(gate))) * up;
+        }
+        *reinterpret_cast<uint2*>(dst + kTile * h) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+      }
+    }
+  }
+}
+
+// ---- launch plans -----------------------------------------------------------
+
+int shape_status(int64_t rows, int64_t k, int64_t n) {
+  if (rows < 1 || rows > kMaxRows || k <= 0 || n <= 0) return QF_E_SHAPE;
+  if (k % kChunk != 0 || n % kColAlign != 0) return QF_E_SHAPE;
+  if (k > (int64_t)INT32_MAX || n > (int64_t)INT32_MAX / 2) return QF_E_SHAPE;
+  return QF_OK;
+}
+
+// Power-of-two K splits (measured on the Qwen3-4B projection shapes):
+// as many as keep every wave at least one chunk, the grid at most 3072
+// workgroups of 16 columns (~12 per CU), and the partials (written here, read
+// by the consumer) small: splits * min(M, 16) <= K / 32.
+int plan_splits(int64_t rows, int64_t k, int64_t n) {
+  const int64_t chunks = k / kChunk;
+  const int64_t tiles = n / kTile;
+  const int64_t mrows = rows < kTile ? rows : kTile;
+  int64_t s = 1;
+  while (chunks % (2 * s) == 0 && chunks / (2 * s) >= kWaves && tiles * 2 * s <= 3072 &&
+         2 * s * mrows <= k / 32)
+    s *= 2;
+  return (int)s;
+}
+
+template <int MT, int NT, int WK, int D, bool PAIRS, bool NTL, bool XT>
+int launch(const SkinnyArgs& a, int splits, hipStream_t s) {
+  constexpr int kColsPerBlock = kTile * (PAIRS ? NT / 2 : NT) * (kWaves / WK);
+  const int64_t grid_x = (a.n + kColsPerBlock - 1) / kColsPerBlock;
+  hipLaunchKernelGGL((skinny_kernel<MT, NT, WK, D, PAIRS, NTL, XT>),
+                     dim3((unsigned)grid_x, (unsigned)splits), dim3(kBlock), 0, s, a);
+  return launch_status();
+}
+
+// Tile plans (measured): up to 4 rows of x arrive as one broadcast line per
+// load, so x goes straight into MFMA layout; beyond that x is loaded like W
+// and transposed through LDS.  Larger M shares each x fragment across two
+// n-tiles per wave.
+int dispatch_partials(const SkinnyArgs& a, int splits, hipStream_t s) {
+  switch ((a.m + kTile - 1) / kTile) {
+    case 1:
+      if (a.m <= 4) return launch<1, 1, 4, 2, false, true, false>(a, splits, s);
+      if (a.n / kTile >= 256) return launch<1, 2, 4, 2, false, true, true>(a, splits, s);
+      return launch<1, 1, 4, 2, false, true, true>(a, splits, s);
+    case 2: return launch<2, 2, 4, 2, false, true, true>(a, splits, s);
+    case 3: return launch<3, 2, 4, 2, false, true, true>(a, splits, s);
+    default: return launch<4, 2, 4, 2, false, true, true>(a, splits, s);
+  }
+}
+
+int dispatch_silu(const SkinnyArgs& a, hipStream_t s) {
+  switch ((a.m + kTile - 1) / kTile) {
+    case 1:
+      if (a.m <= 4) return launch<1, 2, 4, 4, true, true, false>(a, 1, s);
+      return launch<1, 2, 4, 4, true, true, true>(a, 1, s);
+    case 2: return launch<2, 2, 4, 2, true, true, true>(a, 1, s);
+    case 3: return launch<3, 2, 4, 2, true, true, true>(a, 1, s);
+    default: return launch<4, 2, 4, 2, true, true, true>(a, 1, s);
+  }
+}
+
+}  // namespace
+}  // namespace qf
+
+using namespace qf;
+
+extern "C" int qf_linear_splits(int64_t rows, int64_t k, int64_t n) {
+  const int st = shape_status(rows, k, n);
+  return st != QF_OK ? st : plan_splits(rows, k, n);
+}
+
+extern "C" int qf_linear_partials(const void* x, int64_t rows, int64_t k, const void* weight,
+                                  int64_t n, int32_t splits, void* partials, void* stream) {
+  const int st = shape_status(rows, k, n);
+  if (st != QF_OK) return st;
+  if (!x || !weight || !partials) return QF_E_ARG;
+  if (splits < 1 || (k / kChunk) % splits != 0) return QF_E_ARG;
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(partials)) return QF_E_ALIGN;
+  SkinnyArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(weight);
+  a.partials = static_cast<float*>(partials);
+  a.out = nullptr;
+  a.k = k;
+  a.m = (int32_t)rows;
+  a.n = (int32_t)n;
+  a.chunks = (int32_t)(k / kChunk / splits);
+  return dispatch_partials(a, splits, as_stream(stream));
+}
+
+extern "C" int qf_linear_silu_mul(const void* x, int64_t rows, int64_t k, const void* gate_up,
+                                  int64_t n, void* out, void* stream) {
+  const int st = shape_status(rows, k, n);
+  if (st != QF_OK) return st;
+  if (!x || !gate_up || !out) return QF_E_ARG;
+  if (!aligned16(x) || !aligned16(gate_up) || (reinterpret_cast<uintptr_t>(out) & 7u) != 0)
+    return QF_E_ALIGN;
+  SkinnyArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(gate_up);
+  a.partials = nullptr;
+  a.out = static_cast<uint16_t*>(out);
+  a.k = k;
+  a.m = (int32_t)rows;
+  a.n = (int32_t)n;
+  a.chunks = (int32_t)(k / kChunk);
+  return dispatch_silu(a, as_stream(stream));
+}

@@ -39,6 +39,9 @@ SIGNATURES = {
                         _vp, _vp, _vp], _i32),
     "qf_embedding": ([_vp, _i64, _vp, _i64, _i64, _vp, _vp], _i32),
     "qf_rope_table": ([_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp], _i32),
+    "qf_linear_splits": ([_i64, _i64, _i64], _i32),
+    "qf_linear_partials": ([_vp, _i64, _i64, _vp, _i64, _i32, _vp, _vp], _i32),
+    "qf_linear_silu_mul": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp], _i32),
 }
 
 _handle: ctypes.CDLL | None = None

@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 10
+    assert len(names) == 13
 
 
 def test_library_exports_every_symbol():
@@ -68,6 +68,18 @@ def test_host_side_argument_errors_launch_nothing():
                               bogus, bogus, bogus, None) == -2
     assert lib.qf_embedding(bogus + 4, 3, bogus, 10, 8, bogus, None) == -3
     assert lib.qf_rope_table(bogus, 0, None, 0, 4, bogus, bogus, None) == -1
+    # split-K projections: the shape rule, the split rule and alignment
+    assert lib.qf_linear_splits(0, 2560, 6144) == -2
+    assert lib.qf_linear_splits(65, 2560, 6144) == -2
+    assert lib.qf_linear_splits(4, 2570, 6144) == -2
+    assert lib.qf_linear_splits(4, 2560, 6160) == -2
+    assert lib.qf_linear_partials(bogus, 4, 2560, bogus, 6144, 3, bogus, None) == -1
+    assert lib.qf_linear_partials(bogus, 4, 2560, bogus, 6144, 0, bogus, None) == -1
+    assert lib.qf_linear_partials(None, 4, 2560, bogus, 6144, 1, bogus, None) == -1
+    assert lib.qf_linear_partials(bogus + 8, 4, 2560, bogus, 6144, 1, bogus, None) == -3
+    assert lib.qf_linear_partials(bogus, 65, 2560, bogus, 6144, 1, bogus, None) == -2
+    assert lib.qf_linear_silu_mul(bogus, 4, 2560, bogus, 9728, bogus + 4, None) == -3
+    assert lib.qf_linear_silu_mul(bogus, 4, 2560, bogus, 9720, bogus, None) == -2
 
 
 def test_empty_inputs_are_no_ops():

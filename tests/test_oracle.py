@@ -402,3 +402,84 @@ def test_silu_mul_golden(golden):
 def test_embedding_golden(golden):
     d = golden["embedding"]
     assert np.array_equal(O.embedding(d["ids"], d["table"]), d["out"])
+
+
+# ------------------------------------------------------- decode projections
+
+def _ints(shape, lo, hi, g):
+    return torch.randint(lo, hi + 1, shape, generator=g).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("m,n,k,splits", [(1, 32, 64, 1), (3, 64, 256, 4), (16, 96, 192, 3),
+                                          (17, 32, 128, 2), (64, 64, 640, 10)])
+def test_linear_partials_integer_known_answer(m, n, k, splits):
+    # Small integers: every partial sum is an exact f32, so the oracle must equal
+    # an int64 matmul of each K chunk bit for bit (pins indexing and the split).
+    g = gen(40)
+    x, w = _ints((m, k), -4, 4, g), _ints((n, k), -4, 4, g)
+    got = O.linear_partials(bits(x), bits(w), splits)
+    xi, wi = x.to(torch.int64), w.to(torch.int64)
+    per = k // splits
+    for s in range(splits):
+        chunk = slice(s * per, (s + 1) * per)
+        np.testing.assert_array_equal(got[s], (xi[:, chunk] @ wi[:, chunk].T).numpy().astype(np.float32))
+
+
+def test_linear_partials_match_torch_float64():
+    g = gen(41)
+    x, w = normal((5, 512), g=g), normal((64, 512), 0.0, 0.05, g)
+    got = O.linear_partials(bits(x), bits(w), 4)
+    for s in range(4):
+        chunk = slice(128 * s, 128 * (s + 1))
+        exact = F.linear(x[:, chunk].double(), w[:, chunk].double()).float().numpy()
+        np.testing.assert_array_equal(got[s], exact)  # exactly rounded, like float64 -> f32
+    # the consumer's sum equals the full-K product up to f32 summation error
+    full = F.linear(x.double(), w.double()).numpy()
+    scale = (x.double().abs() @ w.double().abs().T).numpy()
+    assert (np.abs(got.astype(np.float64).sum(0) - full) <= 4 * 2.0**-24 * scale + 1e-30).all()
+
+
+def test_linear_partials_planted_mistakes_are_caught():
+    g = gen(42)
+    x, w = normal((4, 256), g=g), normal((32, 256), g=g)
+    good = O.linear_partials(bits(x), bits(w), 2)
+    exact = F.linear(x.double(), w.double()).numpy()
+    # a dropped last 32-wide k step
+    dropped = F.linear(x[:, :-32].double(), w[:, :-32].double()).numpy()
+    # mismatched fragment layouts: x's k-group 8g..8g+7 against W's k-group g^1
+    perm = torch.arange(256) ^ 8
+    swapped = x.double() @ w.double()[:, perm].T
+    total = good.astype(np.float64).sum(0)
+    tol = 1e-4 * np.abs(exact).max()
+    assert np.abs(total - exact).max() <= tol
+    assert np.abs(dropped - exact).max() > tol
+    assert np.abs(swapped.numpy() - exact).max() > tol
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 32, 128), (4, 64, 256), (16, 32, 640), (33, 32, 64)])
+def test_linear_silu_mul_is_rounded_projections_then_silu_mul(m, n, k):
+    g = gen(43)
+    x = normal((m, k), 0.0, 2.0, g)
+    gate_up = normal((2 * n, k), 0.0, 4.0 / k**0.5, g)
+    got = O.linear_silu_mul(bits(x), bits(gate_up))
+    # bf16 projections, exactly rounded (float64 -> f32 -> bf16), then SiLU * up
+    proj = F.linear(x.double(), gate_up.double()).float().to(torch.bfloat16)
+    np.testing.assert_array_equal(got, O.silu_mul(bits(proj)))
+    # third-party arithmetic: torch F.silu on the bf16 projections
+    gate, up = proj.chunk(2, dim=-1)
+    assert_bf16_close(got, F.silu(gate) * up, max_ulp=1, min_exact=0.99, what="linear_silu_mul")
+
+
+def test_linear_silu_mul_integer_known_answer_and_negative_control():
+    g = gen(44)
+    x, gate_up = _ints((8, 192), -2, 2, g), _ints((64, 192), -1, 1, g)
+    got = O.linear_silu_mul(bits(x), bits(gate_up))
+    proj = (x.to(torch.int64) @ gate_up.to(torch.int64).T).float().to(torch.bfloat16)
+    np.testing.assert_array_equal(got, O.silu_mul(bits(proj)))
+    # The reference's negative control: skipping the bf16 rounding of the
+    # projections is a different function (tests/test_skinny_gemm.py:195-200).
+    x = normal((64, 256), 0.0, 3.0, gen(45))
+    w = normal((128, 256), g=gen(46))
+    gate, up = F.linear(x.float(), w.float()).chunk(2, dim=-1)
+    unrounded = (F.silu(gate) * up).to(torch.bfloat16)
+    assert (O.ulp_distance(O.linear_silu_mul(bits(x), bits(w)), bits(unrounded)) > 0).any()

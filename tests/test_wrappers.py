@@ -288,13 +288,66 @@ def test_fused_embedding_shares_the_weight_parameter():
         embedding.FusedEmbedding(torch.nn.Embedding(10, 8, max_norm=1.0))
 
 
-def test_skinny_gemm_stand_in_declines_every_shape():
-    """engine/decode_step.py:22-30 falls back to F.linear when supports() is False."""
-    from starter_amd.kernels import skinny_gemm
+def test_skinny_supports_is_the_reference_static_rule():
+    """engine/kernels/skinny_gemm.py:75-83; the reference test's cases
+    (tests/test_skinny_gemm.py:183-204) plus the 16-byte start alignment."""
+    from starter_amd.kernels import skinny_gemm as sk
     x, w = Fake((4, 2560)), Fake((6144, 2560))
-    assert skinny_gemm.supports(x, w) is False
-    assert skinny_gemm.supports(x, Fake((19456, 2560)), pairs=True) is False
+    assert sk.supports(x, w)
+    assert sk.supports(Fake((sk.MAX_ROWS, 2560)), w)
+    assert sk.supports(x, Fake((19456, 2560)), pairs=True)
+    for bad_x, bad_w, pairs in (
+        (Fake((sk.MAX_ROWS + 1, 2560)), w, False),
+        (Fake((0, 2560)), w, False),
+        (Fake((4, 2560), cuda=False), Fake((6144, 2560), cuda=False), False),
+        (Fake((4, 2560), dtype=torch.float16), w, False),
+        (Fake((4, 2560), strides=(1, 4)), w, False),
+        (x, Fake((6144, 2560), strides=(1, 6144)), False),
+        (Fake((4, 2570)), Fake((6144, 2570)), False),        # K not a multiple of 64
+        (x, Fake((6144 + 8, 2560)), False),                  # N not a multiple of 32
+        (x, Fake((3 * sk.BN, 2560)), True),                  # pairs need 2*BN
+        (Fake((4, 2560)), Fake((6144, 2561)), False),        # K mismatch
+        (Fake((2, 4, 2560)), w, False),
+        (Fake((4, 2560), ptr=0x100008), w, False),           # misaligned start
+    ):
+        assert not sk.supports(bad_x, bad_w, pairs=pairs)
     with pytest.raises(ValueError):
-        skinny_gemm.linear_partials(x, w)
+        sk._dims(Fake((4, 2560), cuda=False), Fake((6144, 2560), cuda=False))
     with pytest.raises(ValueError):
-        skinny_gemm.linear_silu_mul(x, w)
+        sk.linear_partials(Fake((65, 256)), Fake((64, 256)))
+    with pytest.raises(ValueError):
+        sk.linear_silu_mul(Fake((4, 256)), Fake((96, 256)))
+
+
+def test_skinny_split_plan():
+    """The library's plan: a power of two dividing K/64 that leaves every
+    wave a chunk; fewer splits as rows grow (the partials cost rows * splits)."""
+    from starter_amd.kernels import skinny_gemm as sk
+    qwen = {"qkv": (6144, 2560), "o": (2560, 4096), "down": (2560, 9728)}
+    for n, k in qwen.values():
+        prev = None
+        for rows in (1, 4, 16, 32, 64):
+            s = sk.split_count(n, k, rows)
+            assert s >= 1 and s & (s - 1) == 0 and (k // 64) % s == 0 and k // 64 // s >= 4
+            assert prev is None or s <= prev
+            prev = s
+    assert sk.split_count(6144, 2560, 1) == 8 and sk.split_count(6144, 2560, 16) == 4
+    assert sk.split_count(2560, 4096, 1) == 16 and sk.split_count(2560, 9728, 64) == 8
+    assert sk.split_count(1024, 64, 1) == 1      # one chunk: no split possible
+    with pytest.raises(ValueError):
+        sk.split_count(6144, 2560, 65)
+    with pytest.raises(ValueError):
+        sk.split_count(6144 + 16, 2560, 1)
+
+
+def test_skinny_marshalling():
+    from starter_amd.kernels import skinny_gemm as sk
+    with recorded() as calls:
+        p = sk.linear_partials(Fake((5, 2560)), Fake((6144, 2560)))
+        h = sk.linear_silu_mul(Fake((5, 2560)), Fake((19456, 2560)))
+    assert tuple(p.shape) == (sk.split_count(6144, 2560, 5), 5, 6144) and p.dtype == torch.float32
+    assert tuple(h.shape) == (5, 9728) and h.dtype == BF16
+    name, _, m, k, _, n, splits = calls[0][:7]
+    assert (name, m, k, n, splits) == ("qf_linear_partials", 5, 2560, 6144, p.shape[0])
+    name, _, m, k, _, n = calls[1][:6]
+    assert (name, m, k, n) == ("qf_linear_silu_mul", 5, 2560, 9728)
