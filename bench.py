@@ -16,8 +16,10 @@ The step is replayed from captured HIP graphs (as the engine replays its
 captured prefill), so host launch overhead is not part of the GPU timeline.
 Per-kernel durations come from HIP events around graphs of 24 back-to-back
 launches of one kernel (rotating its buffer sets), divided by 24.  Decode
-configs 1-3 are timed the same way (microseconds per call).  The CPU baseline is the C
-oracle (single thread) on the same step's shapes, timed on this host.
+configs 1-3 are timed the same way (microseconds per call), and so are the
+split-K decode projections of one Qwen3-4B layer at batch 1-64, beside the
+F.linear (hipBLASLt) path they replace.  The CPU baseline is the C oracle
+(single thread) on the same step's shapes, timed on this host.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
 """
@@ -45,6 +47,7 @@ from starter_amd.kernels.prefill import prefill_qkv  # noqa: E402
 from starter_amd.kernels.qk_norm_rope import qk_norm_rope  # noqa: E402
 from starter_amd.kernels.rmsnorm import rms_norm  # noqa: E402
 from starter_amd.kernels.rotary import default_inv_freq, rope_tables  # noqa: E402
+from starter_amd.kernels import skinny_gemm  # noqa: E402
 
 METRIC = ("achieved HBM GB/s (% of MI355X peak) + µs/call per fused kernel, decode & prefill")
 PEAK_GBPS = 8000.0          # MI355X HBM3E, AMD specification
@@ -252,6 +255,62 @@ def decode_configs(device) -> dict:
     return out
 
 
+#: Decode projections of one Qwen3-4B layer: (n, k) of W [n, k]; gate_up is packed [2n, k].
+PROJECTIONS = {"qkv": (6144, 2560), "o_proj": (H, 4096), "gate_up": (I, H), "down": (H, I)}
+PROJECTION_ROWS = (1, 4, 16, 64)
+
+
+def decode_projections(device, replays: int = 20, calls: int = 24) -> dict:
+    """Split-K projections (linear_partials / linear_silu_mul) at decode batch
+    1-64 on the Qwen3-4B layer shapes, next to the unfused path the engine
+    takes without them (F.linear on hipBLASLt, plus silu_mul for gate/up).
+    Weights rotate over enough copies to exceed twice the Infinity Cache, as
+    in decode, where 36 layers of weights (7.3 GB) stream from HBM each step."""
+    g = torch.Generator(device=device).manual_seed(1)
+    out = {}
+    for name, (n, k) in PROJECTIONS.items():
+        rows_w = 2 * n if name == "gate_up" else n
+        w_bytes = bf16_bytes(rows_w * k)
+        weights = [normal((rows_w, k), 0.0, k ** -0.5, g) for _ in range(sets_for(w_bytes))]
+        entry = {}
+        for m in PROJECTION_ROWS:
+            x = normal((m, k), g=g)
+            if name == "gate_up":
+                ours = lambda i, x=x: skinny_gemm.linear_silu_mul(x, weights[i % len(weights)])
+                base = lambda i, x=x: silu_mul(torch.nn.functional.linear(x, weights[i % len(weights)]))
+                out_bytes, splits = bf16_bytes(m * n), 1
+            else:
+                ours = lambda i, x=x: skinny_gemm.linear_partials(x, weights[i % len(weights)])
+                base = lambda i, x=x: torch.nn.functional.linear(x, weights[i % len(weights)])
+                splits = skinny_gemm.split_count(n, k, m)
+                out_bytes = 4 * splits * m * n
+            t_ours = graph_time_rotating(ours, calls, replays)
+            t_base = graph_time_rotating(base, calls, replays)
+            moved = w_bytes + bf16_bytes(m * k) + out_bytes
+            entry[f"m{m}"] = {"us_per_call": t_ours, "bytes": moved, "splits": splits,
+                              "gbps": moved / (t_ours * 1e3), "frac": moved / (t_ours * 1e3) / PEAK_GBPS,
+                              "hipblaslt_us": t_base, "speedup_vs_hipblaslt": t_base / t_ours}
+            print(f"bench: proj {name:8s} m={m:2d} {t_ours:7.2f} us ({100 * entry[f'm{m}']['frac']:.1f}% "
+                  f"of peak)  F.linear path {t_base:7.2f} us", file=sys.stderr, flush=True)
+        out[name] = entry
+        del weights
+        torch.cuda.empty_cache()
+    for m in PROJECTION_ROWS:
+        ours = sum(out[name][f"m{m}"]["us_per_call"] for name in PROJECTIONS)
+        base = sum(out[name][f"m{m}"]["hipblaslt_us"] for name in PROJECTIONS)
+        out[f"layer_m{m}"] = {"us": ours, "hipblaslt_us": base, "speedup_vs_hipblaslt": base / ours}
+    return out
+
+
+def graph_time_rotating(fn, calls: int, replays: int) -> float:
+    """Median microseconds per call of ``fn(i)``, i = 0..calls-1, captured in one graph."""
+    graph = capture(lambda: [fn(i) for i in range(calls)])
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    return statistics.median(t / calls for t in timed_replays(graph, replays))
+
+
 def copy_bandwidth(device) -> float:
     """GB/s of a plain 1 GiB device-to-device copy (read + write counted)."""
     src = torch.empty(1 << 29, dtype=BF16, device=device)
@@ -329,7 +388,8 @@ def pmc_traffic(kernel: str) -> float | None:
 def profile_run(device, launches: int) -> None:
     """Eager launches for counter collection: a calibration copy of known size
     (CALIBRATION_BYTES read + written by torch's copy kernel), then each
-    prefill kernel ``launches`` times on rotating buffer sets."""
+    prefill kernel ``launches`` times on rotating buffer sets, then each decode
+    projection at batch 1 and 16 ``launches`` times on rotating weights."""
     src = torch.empty(CALIBRATION_BYTES // 2, dtype=BF16, device=device).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -342,7 +402,25 @@ def profile_run(device, launches: int) -> None:
         for k in range(launches):
             work.launch(name, k)
         torch.cuda.synchronize()
-    print(json.dumps({"profile": list(KERNELS), "launches": launches,
+    del work
+    torch.cuda.empty_cache()
+    # Decode projections at batch 1 and 16, in this order (dispatch order
+    # tells apart projections that share a kernel instantiation).
+    g = torch.Generator(device=device).manual_seed(1)
+    order = []
+    for name, (n, k) in PROJECTIONS.items():
+        rows_w = 2 * n if name == "gate_up" else n
+        weights = [normal((rows_w, k), 0.0, k ** -0.5, g) for _ in range(sets_for(bf16_bytes(rows_w * k)))]
+        for m in (1, 16):
+            x = normal((m, k), g=g)
+            fn = skinny_gemm.linear_silu_mul if name == "gate_up" else skinny_gemm.linear_partials
+            for i in range(launches):
+                fn(x, weights[i % len(weights)])
+            torch.cuda.synchronize()
+            order.append(f"{name}_m{m}")
+        del weights
+        torch.cuda.empty_cache()
+    print(json.dumps({"profile": list(KERNELS), "projections": order, "launches": launches,
                       "calibration_bytes": CALIBRATION_BYTES}), flush=True)
 
 
@@ -353,6 +431,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode configs")
+    ap.add_argument("--no-proj", action="store_true", help="skip the decode projections")
     ap.add_argument("--profile", type=int, default=0, metavar="N",
                     help="only run a calibration copy and N eager launches per prefill kernel "
                          "(for rocprofv3 --pmc), then exit")
@@ -405,6 +484,7 @@ def main() -> int:
         for name, entry in decode.items():
             print(f"bench: {name:34s} {entry['us_per_call']:6.2f} us/call", file=sys.stderr,
                   flush=True)
+        projections = {} if args.no_proj else decode_projections(device)
 
     dominant = max(KERNELS, key=lambda n: kernels[n]["us_per_call_mean"])
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": kernels[dominant]["gbps"],
@@ -434,6 +514,7 @@ def main() -> int:
         "roofline": roofline,
         "kernels": kernels,
         "decode": decode,
+        "projections": projections,
         "copy_gbps": copy_gbps,
     }
     if not args.no_cpu:
