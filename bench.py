@@ -18,7 +18,8 @@ Per-kernel durations come from HIP events around graphs of 24 back-to-back
 launches of one kernel (rotating its buffer sets), divided by 24.  Decode
 configs 1-3 are timed the same way (microseconds per call), and so are the
 split-K decode projections of one Qwen3-4B layer at batch 1-64, beside the
-F.linear (hipBLASLt) path they replace.  The CPU baseline is the C oracle
+F.linear (hipBLASLt) path they replace, and decode attention at the engine
+contract's public workloads beside torch's scaled_dot_product_attention.  The CPU baseline is the C oracle
 (single thread) on the same step's shapes, timed on this host.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
@@ -48,6 +49,7 @@ from starter_amd.kernels.qk_norm_rope import qk_norm_rope  # noqa: E402
 from starter_amd.kernels.rmsnorm import rms_norm  # noqa: E402
 from starter_amd.kernels.rotary import default_inv_freq, rope_tables  # noqa: E402
 from starter_amd.kernels import skinny_gemm  # noqa: E402
+from starter_amd.kernels.small_query_attention import SmallQueryAttention  # noqa: E402
 
 METRIC = ("achieved HBM GB/s (% of MI355X peak) + µs/call per fused kernel, decode & prefill")
 PEAK_GBPS = 8000.0          # MI355X HBM3E, AMD specification
@@ -302,6 +304,47 @@ def decode_projections(device, replays: int = 20, calls: int = 24) -> dict:
     return out
 
 
+#: Decode attention of the contract's public workloads (batch, prompt + output
+#: tokens + 1): every used key of every layer is read once per step.
+ATTENTION_CASES = ((1, 545), (4, 2081), (16, 641))
+
+
+def decode_attention_bench(device, replays: int = 20, calls: int = 24) -> dict:
+    """SmallQueryAttention.run at full cache length on the Qwen3-4B head
+    layout (32 query heads, 8 KV heads, width 128), K/V rotating over copies
+    beyond twice the Infinity Cache; beside torch's scaled_dot_product_attention
+    with GQA on the same tensors (the engine's other GPU path is torch's own
+    flash attention)."""
+    g = torch.Generator(device=device).manual_seed(2)
+    out = {}
+    for batch, cap in ATTENTION_CASES:
+        kv_bytes = bf16_bytes(2 * batch * NK * cap * D)
+        sets = sets_for(kv_bytes)
+        caches = [(normal((batch, NK, cap, D), g=g), normal((batch, NK, cap, D), g=g)) for _ in range(sets)]
+        q = normal((batch, NQ, 1, D), g=g)
+        used = torch.full((batch * NK,), cap, dtype=torch.int32, device=device)
+        plan = SmallQueryAttention(batch, NQ, NK, cap, device)
+        ours = lambda i: plan.run(q, *caches[i % sets], used, D ** -0.5)
+        base = lambda i: torch.nn.functional.scaled_dot_product_attention(
+            q, *caches[i % sets], scale=D ** -0.5, enable_gqa=True)
+        t_ours = graph_time_rotating(ours, calls, replays)
+        try:
+            t_base = graph_time_rotating(base, calls, replays)
+        except RuntimeError:
+            t_base = None
+        moved = kv_bytes + bf16_bytes(2 * batch * NQ * D)
+        key = f"b{batch}_ctx{cap}"
+        out[key] = {"us_per_call": t_ours, "bytes": moved, "splits": plan.splits,
+                    "gbps": moved / (t_ours * 1e3), "frac": moved / (t_ours * 1e3) / PEAK_GBPS,
+                    "torch_sdpa_us": t_base}
+        print(f"bench: attention {key:12s} {t_ours:7.2f} us ({100 * out[key]['frac']:.1f}% of peak, "
+              f"{plan.splits} splits)  torch sdpa {t_base if t_base is None else round(t_base, 2)} us",
+              file=sys.stderr, flush=True)
+        del caches
+        torch.cuda.empty_cache()
+    return out
+
+
 def graph_time_rotating(fn, calls: int, replays: int) -> float:
     """Median microseconds per call of ``fn(i)``, i = 0..calls-1, captured in one graph."""
     graph = capture(lambda: [fn(i) for i in range(calls)])
@@ -431,7 +474,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode configs")
-    ap.add_argument("--no-proj", action="store_true", help="skip the decode projections")
+    ap.add_argument("--no-proj", action="store_true",
+                    help="skip the decode projections and decode attention")
     ap.add_argument("--profile", type=int, default=0, metavar="N",
                     help="only run a calibration copy and N eager launches per prefill kernel "
                          "(for rocprofv3 --pmc), then exit")
@@ -485,6 +529,7 @@ def main() -> int:
             print(f"bench: {name:34s} {entry['us_per_call']:6.2f} us/call", file=sys.stderr,
                   flush=True)
         projections = {} if args.no_proj else decode_projections(device)
+        attention = {} if args.no_proj else decode_attention_bench(device)
 
     dominant = max(KERNELS, key=lambda n: kernels[n]["us_per_call_mean"])
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": kernels[dominant]["gbps"],
@@ -515,6 +560,7 @@ def main() -> int:
         "kernels": kernels,
         "decode": decode,
         "projections": projections,
+        "attention": attention,
         "copy_gbps": copy_gbps,
     }
     if not args.no_cpu:

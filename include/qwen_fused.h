@@ -2,8 +2,9 @@
  * qwen_fused.h - C ABI of the MI355X (gfx950) fused layer kernels of the
  * Qwen3-4B decode engine: residual-add + RMSNorm, per-head Q/K RMSNorm fused
  * with NeoX rotary embedding (three layouts), SiLU(gate)*up, the token
- * embedding gather, the rotary cos/sin table builder, and the split-K decode
- * projections that feed the fused consumers.
+ * embedding gather, the rotary cos/sin table builder, the split-K decode
+ * projections that feed the fused consumers, and grouped-query decode
+ * attention over the K/V cache.
  *
  * Conventions shared by every entry point:
  *   - Tensors are plain device pointers.  "bf16" buffers hold IEEE bfloat16
@@ -195,6 +196,41 @@ int qf_linear_partials(const void* x, int64_t rows, int64_t k, const void* weigh
  */
 int qf_linear_silu_mul(const void* x, int64_t rows, int64_t k, const void* gate_up,
                        int64_t n, void* out, void* stream);
+
+/*
+ * Key-segment plan of qf_decode_attention for virtual_heads = batch * Hkv
+ * heads of a cache with `capacity` slots on a GPU with compute_units CUs:
+ * about two workgroups per CU, segments of whole 64-key tiles, at most 32.
+ * Writes *splits >= 1 and *span (keys per segment, a multiple of 64) with
+ * (splits - 1) * span < capacity <= splits * span.
+ * Replaces partition_keys (engine/kernels/small_query_attention.py:24-38).
+ */
+int qf_attention_partition(int64_t virtual_heads, int64_t capacity, int32_t compute_units,
+                           int32_t* splits, int64_t* span);
+
+/*
+ * Decode attention, one query token per sequence, grouped-query heads:
+ *   q bf16 [batch, q_heads, 1, 128]; k, v bf16 [batch, kv_heads, capacity, 128]
+ *   (all contiguous); used int32 [batch * kv_heads] on the device: keys
+ *   0 .. used-1 of each (sequence, kv head) are attended (clamped to
+ *   [0, capacity]); slots at or beyond used are never read.
+ *   Query head h of sequence b reads kv head h / (q_heads / kv_heads).
+ *   s = (q . k) * scale; out = softmax(s) @ v with f32 statistics, the
+ *   probabilities rounded to bf16 before they multiply v, the result rounded
+ *   once to bf16; no valid key -> zeros.  out bf16 [batch, 1, q_heads, 128].
+ * q_heads / kv_heads <= 16.  (splits, span) as qf_attention_partition gives
+ * (any split of the capacity into whole 16-key multiples works).  splits > 1
+ * needs scratch: partials f32 [batch*kv_heads, splits, G, 128] and stats f32
+ * [batch*kv_heads, splits, 2, G] (G = q_heads / kv_heads); calls sharing it
+ * must be ordered on one stream.  One launch per 8 query rows of a group
+ * (one for Qwen3's G = 4), plus a merge launch when splits > 1.
+ * Replaces SmallQueryAttention.run + _segments + _merge
+ * (engine/kernels/small_query_attention.py:41-110, 135-158).
+ */
+int qf_decode_attention(const void* q, const void* k, const void* v, const int32_t* used,
+                        int64_t batch, int32_t q_heads, int32_t kv_heads, int64_t capacity,
+                        float scale, int32_t splits, int64_t span, float* partials,
+                        float* stats, void* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,8 @@ _SIGNATURES = {
     "or_rope_table": ([_vp, _i32, _vp, _i64, _i64, _vp, _vp], None),
     "or_linear_partials": ([_vp, _i64, _i64, _vp, _i64, _i32, _vp], None),
     "or_linear_silu_mul": ([_vp, _i64, _i64, _vp, _i64, _vp], None),
+    "or_decode_attention": ([_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, ctypes.c_double, _vp, _vp],
+                            None),
 }
 
 
@@ -246,4 +248,19 @@ def linear_silu_mul(x, gate_up) -> np.ndarray:
         raise ValueError("linear_silu_mul: shapes disagree")
     out = np.empty((m, width // 2), dtype=np.uint16)
     lib().or_linear_silu_mul(_p(x), m, k, _p(gate_up), width // 2, _p(out))
+    return out
+
+
+def decode_attention(q, k, v, used, scale: float) -> np.ndarray:
+    """engine/kernels/small_query_attention.py:113-158 in float64: q bits
+    [B, Hq, 1, 128], k/v bits [B, Hkv, C, 128], used int32 [B*Hkv].
+    Returns bf16 bits [B, 1, Hq, 128]."""
+    q, k, v = _u16(q), _u16(k), _u16(v)
+    used = np.ascontiguousarray(used, dtype=np.int32)
+    batch, hq = q.shape[0], q.shape[1]
+    hk, capacity = k.shape[1], k.shape[2]
+    out = np.empty((batch, 1, hq, 128), dtype=np.uint16)
+    scratch = np.empty(max(capacity, 1), dtype=np.float64)
+    lib().or_decode_attention(_p(q), _p(k), _p(v), _p(used), batch, hq, hk, capacity, float(scale),
+                              _p(scratch), _p(out))
     return out

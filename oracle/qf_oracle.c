@@ -37,6 +37,10 @@
  *                          per split; torch float64 F.linear per chunk;
  *                          dropped-chunk and transposed-operand mistakes
  *                          must be detected.
+ *   or_decode_attention    torch float64 softmax attention per (sequence, kv
+ *                          head); known answers (zero queries -> mean of V,
+ *                          one dominant key block -> its V); wrong head
+ *                          mapping and reading past `used` are detected.
  *   or_linear_silu_mul     composition of exactly rounded projections with
  *                          or_silu_mul (bit-exact), torch float64 projections
  *                          + F.silu; skipping the projection rounding must
@@ -359,5 +363,45 @@ EXPORT void or_linear_silu_mul(const uint16_t* x, int64_t m, int64_t k, const ui
       const float u = rbf(dot_f32(x + i * k, gate_up + (n + j) * k, 0, k));
       const float act = rbf(g / (1.0f + expf(-g)));
       out[i * n + j] = or_bf16(act * u);
+    }
+}
+
+/* ------------------------------------------------------ decode attention */
+
+/* engine/kernels/small_query_attention.py:113-158 (the function it computes;
+ * its tests' float64 restatement is tests/test_small_query_attention.py:
+ * 151-163): for query head h of sequence b, kv head h / G (G = hq / hk),
+ *   out = bf16( softmax((q . k_j) * scale over j < used) @ v )
+ * in double; no valid key -> zeros.  q [b*hq, 128], k/v [b*hk*capacity, 128],
+ * used [b*hk], out [b*hq, 128].  Keys at or beyond used are not read. */
+EXPORT void or_decode_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                const int32_t* used, int64_t batch, int32_t hq, int32_t hk,
+                                int64_t capacity, double scale, double* scratch, uint16_t* out) {
+  const int32_t groups = hq / hk;
+  for (int64_t b = 0; b < batch; ++b)
+    for (int32_t h = 0; h < hq; ++h) {
+      const int64_t vh = b * hk + h / groups;
+      int64_t n = used[vh];
+      if (n < 0) n = 0;
+      if (n > capacity) n = capacity;
+      const uint16_t* qr = q + (b * hq + h) * HEAD;
+      uint16_t* o = out + (b * hq + h) * HEAD;
+      double mx = -INFINITY;
+      for (int64_t j = 0; j < n; ++j) {
+        const uint16_t* kr = k + (vh * capacity + j) * HEAD;
+        double dot = 0.0;
+        for (int d = 0; d < HEAD; ++d) dot += (double)or_f32(qr[d]) * (double)or_f32(kr[d]);
+        scratch[j] = dot * scale;
+        if (scratch[j] > mx) mx = scratch[j];
+      }
+      double acc[HEAD] = {0};
+      double den = 0.0;
+      for (int64_t j = 0; j < n; ++j) {
+        const double p = exp(scratch[j] - mx);
+        den += p;
+        const uint16_t* vr = v + (vh * capacity + j) * HEAD;
+        for (int d = 0; d < HEAD; ++d) acc[d] += p * (double)or_f32(vr[d]);
+      }
+      for (int d = 0; d < HEAD; ++d) o[d] = n ? or_bf16((float)(acc[d] / den)) : 0;
     }
 }

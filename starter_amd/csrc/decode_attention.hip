@@ -1,0 +1,385 @@
+// Grouped-query decode attention for gfx950: one query token per sequence
+// against the head-major K/V cache, split over key segments with an f32
+// merge (engine/kernels/small_query_attention.py:41-110 is the reference:
+// _segments :41-86, _merge :89-110).
+//
+// A virtual head vh = batch * Hkv + kv_head owns G = Hq / Hkv query rows
+// (flattened query row vh * G + g) and the first used[vh] keys of its cache
+// rows [vh * capacity, ...).  Per query row, with s = (q . k) * scale * log2 e:
+//   out = sum_k bf16(2^(s_k - m)) * v_k / sum_k 2^(s_k - m),  m = max_k s_k
+// evaluated online: each key segment keeps a running maximum m, f32
+// denominator l and f32 numerator, rescaled by 2^(m_old - m_new) as the
+// maximum grows; the probabilities that multiply V are rounded to bf16 first
+// (as the reference feeds them to a bf16 dot) while l sums them in f32.
+// Segments are merged with weights 2^(m_s - M), in segment order, by a
+// second small kernel; only the merged result is rounded to bf16.  Keys at or beyond used[vh] are never loaded, so stale
+// values (NaN poison included) in unused cache slots stay invisible.
+//
+// Layout (HBM-bound: every K/V byte of the used prefix is read once, ~4
+// flops per byte): a wave reads 4 consecutive keys per 16-byte load - 16
+// lanes per 256-byte key row, lane r holding d = 8r .. 8r+8 - so every load
+// is one contiguous KiB.  Scores use v_dot2c_f32_bf16 on the packed bf16
+// pairs and a 16-lane DPP sum; the numerator update is f32 FMAs.  The 16
+// lane groups of a workgroup (4 per wave x 4 waves) take interleaved keys of
+// the segment, each with its own running state, and are merged in lane-group
+// then wave order at the end.
+#include "qf_device.h"
+
+namespace qf {
+namespace {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kD = 128;
+constexpr int kKeysPerWave = 4;                       // one 1 KiB load = 4 key rows
+constexpr int kWavesA = kBlock / kWave;
+constexpr int kKeysPerIter = kKeysPerWave * kWavesA;  // 16 keys per workgroup step
+constexpr int kMaxGroups = 16;
+constexpr int kMaxSplits = 32;
+constexpr float kNegInf = -__builtin_inff();
+
+struct AttnArgs {
+  const uint16_t* q;     // [vh * G, 128]
+  const uint16_t* k;     // [vh * capacity, 128]
+  const uint16_t* v;
+  const int32_t* used;   // [vh]
+  float* partials;       // [vh, S, G, 128]
+  float* stats;          // [vh, S, 2, G]: maxima then denominators
+  uint16_t* out;         // [vh * G, 128]
+  int64_t capacity;
+  int32_t groups;        // G
+  int32_t g0;            // first query row of the group this launch handles
+  int32_t splits;
+  int32_t span;          // keys per segment
+  float scale_log2;      // scale * log2(e)
+};
+
+__device__ __forceinline__ float dpp_f32_sum16(float x) {
+  // All-reduce over aligned 16-lane rows (every lane ends with the sum).
+  x += __uint_as_float(dpp_u32<kQuadXor1>(__float_as_uint(x)));
+  x += __uint_as_float(dpp_u32<kQuadXor2>(__float_as_uint(x)));
+  x += __uint_as_float(dpp_u32<kRowHalfMirror>(__float_as_uint(x)));
+  x += __uint_as_float(dpp_u32<kRowMirror>(__float_as_uint(x)));
+  return x;
+}
+
+__device__ __forceinline__ float dot8(const uint4& a, const uint4& b) {
+  float s = 0.0f;
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.x), __builtin_bit_cast(bf16x2, b.x), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.y), __builtin_bit_cast(bf16x2, b.y), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.z), __builtin_bit_cast(bf16x2, b.z), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.w), __builtin_bit_cast(bf16x2, b.w), s, false);
+  return s;
+}
+
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Running softmax state of one lane group for GT query rows; the lane holds
+// the numerator for d = 8r .. 8r+8.
+template <int GT>
+struct State {
+  float m[GT], l[GT], acc[GT][8];
+};
+
+// Merge one row's state (om, ol, oacc) into row g of `s` (disjoint key sets).
+template <int GT>
+__device__ __forceinline__ void merge_row(State<GT>& s, int g, float om, float ol, const float* oacc) {
+  const float mt = fmaxf(s.m[g], om);
+  if (mt == kNegInf) return;  // both empty
+  const float c1 = exp2_hw(s.m[g] - mt), c2 = exp2_hw(om - mt);
+  s.l[g] = s.l[g] * c1 + ol * c2;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s.acc[g][j] = s.acc[g][j] * c1 + oacc[j] * c2;
+  s.m[g] = mt;
+}
+
+// Merge the state of lane (lane ^ mask) into this lane's.
+template <int GT>
+__device__ __forceinline__ void merge_lanes(State<GT>& s, int mask) {
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    float oacc[8];
+    const float om = __shfl_xor(s.m[g], mask);
+    const float ol = __shfl_xor(s.l[g], mask);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) oacc[j] = __shfl_xor(s.acc[g][j], mask);
+    merge_row<GT>(s, g, om, ol, oacc);
+  }
+}
+
+// One workgroup per (virtual head, key segment), for query rows g0 .. g0+GT-1
+// of the group (those below G); each lane group keeps two sets of U key
+// blocks (4 keys per wave each) in flight.  With one segment the workgroup
+// writes the output; otherwise it writes its f32 partials and statistics for
+// attn_merge_kernel.
+template <int GT, int U>
+__global__ __launch_bounds__(kBlock) void attn_kernel(AttnArgs a) {
+  __shared__ float xm[kWavesA - 1][GT], xl[kWavesA - 1][GT];
+  __shared__ float xacc[kWavesA - 1][GT][kD];
+  const int vh = blockIdx.x;
+  const int seg = blockIdx.y;
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int r = lane % 16;   // d slice 8r .. 8r+8
+  const int q4 = lane / 16;  // key within the wave's 4
+  const int G = a.groups;
+  const int rows = G - a.g0 < GT ? G - a.g0 : GT;  // query rows of this launch
+
+  uint4 qv[GT];
+#pragma unroll
+  for (int g = 0; g < GT; ++g)
+    qv[g] = g < rows ? load16<false>(a.q + ((int64_t)vh * G + a.g0 + g) * kD + 8 * r)
+                     : make_uint4(0, 0, 0, 0);
+
+  int64_t used = a.used[vh];
+  used = used < 0 ? 0 : (used > a.capacity ? a.capacity : used);
+  const int64_t start = (int64_t)seg * a.span;
+  int64_t end = start + a.span;
+  if (end > used) end = used;
+  const uint16_t* kb = a.k + (int64_t)vh * a.capacity * kD + 8 * r;
+  const uint16_t* vb = a.v + (int64_t)vh * a.capacity * kD + 8 * r;
+
+  State<GT> st;
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    st.m[g] = kNegInf;
+    st.l[g] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) st.acc[g][j] = 0.0f;
+  }
+
+  // Block set i of this wave: keys base0 + i*step + q4 + 16u, u < U.
+  constexpr int64_t step = (int64_t)kKeysPerIter * U;
+  const int64_t base0 = start + kKeysPerWave * wave;
+  const int n = base0 < end ? (int)((end - base0 + step - 1) / step) : 0;
+  const int64_t last_key = end - 1;  // a valid slot whenever n > 0
+  uint4 kv[2][U], vv[2][U];
+  // Loads are issued unconditionally (keys past the segment re-read its last
+  // valid key, an L2 hit, and are masked out), so the compiler's wait counts
+  // stay exact and the next set's loads overlap this set's arithmetic.
+  auto issue = [&](int d, int i) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t key = base0 + i * step + q4 + (int64_t)kKeysPerIter * u;
+      const int64_t kc = key < end ? key : last_key;
+      kv[d][u] = load16<false>(kb + kc * kD);
+      vv[d][u] = load16<false>(vb + kc * kD);
+    }
+  };
+  auto consume = [&](int d, int i) {
+    float s[U][GT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool on = base0 + i * step + q4 + (int64_t)kKeysPerIter * u < end;
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        const float dot = dpp_f32_sum16(dot8(qv[g], kv[d][u]));  // all 64 lanes take part
+        s[u][g] = on ? dot * a.scale_log2 : kNegInf;
+      }
+    }
+    float vf[U][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u) unpack8(vv[d][u], vf[u]);
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      float mb = s[0][g];
+#pragma unroll
+      for (int u = 1; u < U; ++u) mb = fmaxf(mb, s[u][g]);
+      const float mn = fmaxf(st.m[g], mb);
+      if (mn == kNegInf) continue;  // no valid key yet in this lane group
+      const float corr = exp2_hw(st.m[g] - mn);
+      float lsum = st.l[g] * corr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) st.acc[g][j] *= corr;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float p = exp2_hw(s[u][g] - mn);  // 0 for a masked key
+        lsum += p;
+        const float pb = from_bf16(to_bf16(p));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st.acc[g][j] = __builtin_fmaf(pb, vf[u][j], st.acc[g][j]);
+      }
+      st.l[g] = lsum;
+      st.m[g] = mn;
+    }
+  };
+  if (n > 0) {
+    issue(0, 0);
+    for (int i = 0;; i += 2) {
+      issue(1, i + 1);
+      consume(0, i);
+      if (i + 1 >= n) break;
+      issue(0, i + 2);
+      consume(1, i + 1);
+      if (i + 2 >= n) break;
+    }
+  }
+
+  // Lane groups of a wave (lanes r, r+16, r+32, r+48 hold the same d slice).
+  merge_lanes<GT>(st, 16);
+  merge_lanes<GT>(st, 32);
+  // Waves 1..3 hand over to wave 0 (lanes 0..15 carry the 128-wide slices).
+  if (wave > 0 && lane < 16) {
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (lane == 0) {
+        xm[wave - 1][g] = st.m[g];
+        xl[wave - 1][g] = st.l[g];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xacc[wave - 1][g][8 * r + j] = st.acc[g][j];
+    }
+  }
+  __syncthreads();
+  const bool owner = wave == 0 && lane < 16;
+  if (owner) {
+#pragma unroll
+    for (int w = 0; w < kWavesA - 1; ++w)
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        float oacc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) oacc[j] = xacc[w][g][8 * r + j];
+        merge_row<GT>(st, g, xm[w][g], xl[w][g], oacc);
+      }
+  }
+
+  if (a.splits == 1) {
+    if (!owner) return;
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (g >= rows) break;
+      const float den = st.l[g] > 0.0f ? st.l[g] : 1.0f;
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = st.acc[g][j] / den;
+      store16<false>(a.out + ((int64_t)vh * G + a.g0 + g) * kD + 8 * r, pack8(o));
+    }
+    return;
+  }
+
+  if (owner) {
+    const int64_t slot = (int64_t)vh * a.splits + seg;
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (g >= rows) break;
+      const int row = a.g0 + g;
+      float* dst = a.partials + (slot * G + row) * kD + 8 * r;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dst[j] = st.acc[g][j];
+      if (r == 0) {
+        a.stats[slot * 2 * G + row] = st.m[g];
+        a.stats[slot * 2 * G + G + row] = st.l[g];
+      }
+    }
+  }
+}
+
+// One 16-lane group per query row (4 rows per wave): weights 2^(m_s - M)
+// for segments with a positive denominator, summed in segment order.
+__global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a, int64_t rows) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 16;
+  const int r = threadIdx.x % 16;
+  if (row >= rows) return;
+  const int G = a.groups;
+  const int64_t vh = row / G;
+  const int g = (int)(row - vh * G);
+  const int S = a.splits;
+  const float* stats = a.stats + vh * S * 2 * G;
+  float M = kNegInf;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, stats[s * 2 * G + g]);
+  if (M == kNegInf) M = 0.0f;
+  float total = 0.0f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int s = 0; s < S; ++s) {
+    const float l = stats[s * 2 * G + G + g];
+    const float w = l > 0.0f ? exp2_hw(stats[s * 2 * G + g] - M) : 0.0f;
+    total += l * w;
+    const float* p = a.partials + ((vh * S + s) * G + g) * kD + 8 * r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += p[j] * w;
+  }
+  const float den = total > 0.0f ? total : 1.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] /= den;
+  store16<false>(a.out + row * kD + 8 * r, pack8(acc));
+}
+
+template <int GT>
+int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
+  // Two sets of U = 2 key blocks in flight (measured best of U = 2, 4, 8 with
+  // and without the second set).  Groups wider than GT (9..16 rows) take two
+  // launches of 8 rows each.
+  constexpr int U = 2;
+  AttnArgs a = args;
+  int st = QF_OK;
+  for (a.g0 = 0; a.g0 < a.groups && st == QF_OK; a.g0 += GT) {
+    hipLaunchKernelGGL((attn_kernel<GT, U>), dim3((unsigned)vheads, (unsigned)a.splits),
+                       dim3(kBlock), 0, s, a);
+    st = launch_status();
+  }
+  if (st != QF_OK || a.splits == 1) return st;
+  const int64_t rows = vheads * a.groups;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(kWave), 0, s, a, rows);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace qf
+
+using namespace qf;
+
+extern "C" int qf_attention_partition(int64_t virtual_heads, int64_t capacity,
+                                      int32_t compute_units, int32_t* splits, int64_t* span) {
+  if (virtual_heads < 1 || capacity < 1 || compute_units < 1 || !splits || !span) return QF_E_ARG;
+  // About two workgroups per compute unit (measured against four and eight:
+  // more segments cost more than they hide), at least one 64-key tile per
+  // segment, at most 32 segments; segments are whole 64-key tiles.
+  const int64_t tiles = (capacity + 63) / 64;
+  const int64_t desired = (2 * (int64_t)compute_units + virtual_heads - 1) / virtual_heads;
+  int64_t s = desired < 1 ? 1 : desired;
+  if (s > tiles) s = tiles;
+  if (s > kMaxSplits) s = kMaxSplits;
+  const int64_t per = (tiles + s - 1) / s;
+  *splits = (int32_t)((tiles + per - 1) / per);
+  *span = per * 64;
+  return QF_OK;
+}
+
+extern "C" int qf_decode_attention(const void* q, const void* k, const void* v,
+                                   const int32_t* used, int64_t batch, int32_t q_heads,
+                                   int32_t kv_heads, int64_t capacity, float scale,
+                                   int32_t splits, int64_t span, float* partials, float* stats,
+                                   void* out, void* stream) {
+  if (batch < 1 || q_heads < 1 || kv_heads < 1 || capacity < 1) return QF_E_ARG;
+  if (q_heads % kv_heads != 0 || q_heads / kv_heads > kMaxGroups) return QF_E_SHAPE;
+  if (!q || !k || !v || !used || !out) return QF_E_ARG;
+  if (splits < 1 || splits > kMaxSplits || span < 1 || span % kKeysPerIter != 0 ||
+      (int64_t)splits * span < capacity || (int64_t)(splits - 1) * span >= capacity)
+    return QF_E_ARG;
+  if (splits > 1 && (!partials || !stats)) return QF_E_ARG;
+  if (!(scale == scale) || scale == __builtin_inff() || scale == kNegInf) return QF_E_ARG;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return QF_E_ALIGN;
+  const int64_t vheads = batch * kv_heads;
+  if (vheads > INT32_MAX) return QF_E_SHAPE;
+  AttnArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.used = used;
+  a.partials = partials;
+  a.stats = stats;
+  a.out = static_cast<uint16_t*>(out);
+  a.capacity = capacity;
+  a.groups = q_heads / kv_heads;
+  a.g0 = 0;
+  a.splits = splits;
+  a.span = (int32_t)span;
+  a.scale_log2 = (float)((double)scale * 1.4426950408889634);
+  hipStream_t s = as_stream(stream);
+  switch (a.groups) {
+    case 1: return launch_attn<1>(a, vheads, s);
+    case 2: return launch_attn<2>(a, vheads, s);
+    case 3: case 4: return launch_attn<4>(a, vheads, s);
+    default: return launch_attn<8>(a, vheads, s);
+  }
+}

@@ -1,0 +1,86 @@
+"""Grouped-query decode attention on gfx950 (split-KV with an f32 merge).
+
+Drop-in for ``engine/kernels/small_query_attention.py`` (jadenpxrk/starter),
+which ``engine/flash_decode.py:48-52`` imports for CUDA GQA with at most 16
+query heads per KV head: ``partition_keys`` and ``SmallQueryAttention`` keep
+their names, signatures, ``ValueError`` rules, scratch ownership (one context
+per instance, calls serialised on one stream) and fresh output allocation.
+
+One query token per sequence attends the first ``used[b * Hkv + h]`` keys of
+its KV head in the head-major cache; slots beyond that are never read.
+Softmax statistics and the value accumulation stay f32; the probabilities
+that multiply V are rounded to bf16 and only the merged output is rounded to
+bf16 (engine/kernels/small_query_attention.py:1-9).  The work launches on
+torch's current stream with no host sync, so a captured decode step replays
+it with fresh ``used`` lengths.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+QUERY_TILE = 16   # most query heads per KV head (engine/kernels/small_query_attention.py:18)
+KEY_TILE = 64     # segment granularity in keys
+MAX_SPLITS = 32
+HEAD = 128
+
+
+def partition_keys(virtual_heads, capacity, multiprocessors):
+    """(splits, span): key segments of whole KEY_TILE tiles covering capacity,
+    about two workgroups per compute unit, at most MAX_SPLITS.  Metadata only;
+    the valid length is read on the device.  Same contract as
+    engine/kernels/small_query_attention.py:24-38."""
+    if min(virtual_heads, capacity, multiprocessors) < 1:
+        raise ValueError("positive head count, capacity and SM count required")
+    splits, span = ctypes.c_int32(), ctypes.c_int64()
+    _lib.call("qf_attention_partition", int(virtual_heads), int(capacity), int(multiprocessors),
+              ctypes.byref(splits), ctypes.byref(span))
+    return splits.value, span.value
+
+
+class SmallQueryAttention:
+    """Fixed-shape, read-only attention; returns fresh [B,1,Hq,128] BF16 output.
+
+    USED is contiguous int32 [B*Hkv], with 0 <= each value <= capacity.
+    Calls must be ordered on one stream; concurrent calls cannot share this
+    instance (its f32 scratch holds the per-segment partials).  Mirrors
+    engine/kernels/small_query_attention.py:113-158.
+    """
+
+    def __init__(self, batch, query_heads, kv_heads, capacity, device):
+        device = torch.device(device)
+        if (device.type != "cuda" or min(batch, query_heads, kv_heads, capacity) < 1
+                or query_heads % kv_heads or not 1 <= query_heads // kv_heads <= QUERY_TILE):
+            raise ValueError("unsupported small-query attention metadata")
+        self.batch, self.hq, self.hk, self.capacity = batch, query_heads, kv_heads, capacity
+        self.groups = query_heads // kv_heads
+        self.virtual_heads = batch * kv_heads
+        units = torch.cuda.get_device_properties(device).multi_processor_count
+        self.splits, self.span = partition_keys(self.virtual_heads, capacity, units)
+        self.partials = torch.empty((self.virtual_heads, self.splits, self.groups, HEAD),
+                                    dtype=torch.float32, device=device)
+        self.stats = torch.empty((self.virtual_heads, self.splits, 2, self.groups),
+                                 dtype=torch.float32, device=device)
+
+    def run(self, query, key, value, used, scale):
+        device = self.partials.device
+        if (torch.is_grad_enabled() or not math.isfinite(scale)
+                or query.shape != (self.batch, self.hq, 1, HEAD)
+                or key.shape != (self.batch, self.hk, self.capacity, HEAD)
+                or value.shape != key.shape
+                or used.shape != (self.virtual_heads,) or used.dtype != torch.int32
+                or used.device != device or not used.is_contiguous()
+                or any(t.dtype != torch.bfloat16 or t.device != device or not t.is_contiguous()
+                       for t in (query, key, value))):
+            raise ValueError("expected fixed-shape contiguous BF16 CUDA Q/K/V and int32 lengths")
+        out = torch.empty((self.batch, 1, self.hq, HEAD), dtype=torch.bfloat16, device=device)
+        _lib.call("qf_decode_attention", query.data_ptr(), key.data_ptr(), value.data_ptr(),
+                  used.data_ptr(), self.batch, self.hq, self.hk, self.capacity, float(scale),
+                  self.splits, self.span, self.partials.data_ptr(), self.stats.data_ptr(),
+                  out.data_ptr(), _lib.stream(device))
+        return out

@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 13
+    assert len(names) == 15
 
 
 def test_library_exports_every_symbol():
@@ -80,6 +80,22 @@ def test_host_side_argument_errors_launch_nothing():
     assert lib.qf_linear_partials(bogus, 65, 2560, bogus, 6144, 1, bogus, None) == -2
     assert lib.qf_linear_silu_mul(bogus, 4, 2560, bogus, 9728, bogus + 4, None) == -3
     assert lib.qf_linear_silu_mul(bogus, 4, 2560, bogus, 9720, bogus, None) == -2
+    # decode attention: group size, split plan, scale, alignment
+    split, span = ctypes.c_int32(), ctypes.c_int64()
+    assert lib.qf_attention_partition(0, 64, 256, ctypes.byref(split), ctypes.byref(span)) == -1
+    assert lib.qf_attention_partition(8, 545, 256, None, ctypes.byref(span)) == -1
+    assert lib.qf_decode_attention(bogus, bogus, bogus, bogus, 1, 34, 2, 64, 0.1, 1, 64, None, None,
+                                   bogus, None) == -2
+    assert lib.qf_decode_attention(bogus, bogus, bogus, bogus, 1, 8, 3, 64, 0.1, 1, 64, None, None,
+                                   bogus, None) == -2
+    assert lib.qf_decode_attention(bogus, bogus, bogus, bogus, 1, 8, 2, 545, 0.1, 1, 64, None, None,
+                                   bogus, None) == -1                 # span does not cover capacity
+    assert lib.qf_decode_attention(bogus, bogus, bogus, bogus, 1, 8, 2, 545, 0.1, 9, 64, None, None,
+                                   bogus, None) == -1                 # splits > 1 needs scratch
+    assert lib.qf_decode_attention(bogus, bogus, bogus, bogus, 1, 8, 2, 64, float("nan"), 1, 64,
+                                   None, None, bogus, None) == -1
+    assert lib.qf_decode_attention(bogus + 2, bogus, bogus, bogus, 1, 8, 2, 64, 0.1, 1, 64, None,
+                                   None, bogus, None) == -3
 
 
 def test_empty_inputs_are_no_ops():

@@ -483,3 +483,68 @@ def test_linear_silu_mul_integer_known_answer_and_negative_control():
     gate, up = F.linear(x.float(), w.float()).chunk(2, dim=-1)
     unrounded = (F.silu(gate) * up).to(torch.bfloat16)
     assert (O.ulp_distance(O.linear_silu_mul(bits(x), bits(w)), bits(unrounded)) > 0).any()
+
+
+# --------------------------------------------------------- decode attention
+
+def sdpa64(q, k, v, used):
+    """torch float64 scaled_dot_product_attention per (sequence, kv head)."""
+    batch, hq = q.shape[:2]
+    hk = k.shape[1]
+    g = hq // hk
+    out = torch.zeros((batch, 1, hq, 128), dtype=torch.float64)
+    for b in range(batch):
+        for h in range(hk):
+            n = int(used[b * hk + h])
+            if n:
+                out[b, 0, h * g:(h + 1) * g] = F.scaled_dot_product_attention(
+                    q[b, h * g:(h + 1) * g, 0].double()[None], k[b, h, :n].double()[None],
+                    v[b, h, :n].double()[None], scale=128 ** -0.5)[0]
+    return out
+
+
+@pytest.mark.parametrize("b,hq,hk,cap", [(1, 4, 1, 1), (1, 4, 1, 65), (2, 6, 2, 257), (3, 8, 2, 129),
+                                         (1, 32, 8, 544), (1, 16, 1, 193)])
+def test_decode_attention_matches_torch_float64(b, hq, hk, cap):
+    g = gen(300 + cap)
+    q, k, v = normal((b, hq, 1, 128), g=g), normal((b, hk, cap, 128), g=g), normal((b, hk, cap, 128), g=g)
+    used = (torch.arange(b * hk, dtype=torch.int32) * 37 % (cap + 1)).clamp(min=1)
+    used[0] = cap
+    poisoned_k, poisoned_v = k.clone(), v.clone()
+    for vh in range(b * hk):
+        poisoned_k.view(b * hk, cap, 128)[vh, int(used[vh]):] = float("nan")
+        poisoned_v.view(b * hk, cap, 128)[vh, int(used[vh]):] = float("nan")
+    got = O.decode_attention(bits(q), bits(poisoned_k), bits(poisoned_v), used.numpy(), 128 ** -0.5)
+    assert not np.isnan(O.bf16_value(got)).any()  # slots past `used` are never read
+    expected = sdpa64(q, k, v, used).to(torch.bfloat16)
+    assert_bf16_close(got, expected, max_ulp=1, min_exact=0.999, what="decode attention")
+
+
+def test_decode_attention_known_answers_and_planted_mistakes():
+    # zero queries: uniform weights, so the output is the mean of the valid V rows
+    q = torch.zeros(1, 4, 1, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 1, 193, 128, dtype=torch.bfloat16)
+    v = torch.zeros_like(k)
+    v[:, :, :64], v[:, :, 64:128], v[:, :, 128:] = 2, 6, 20
+    used = np.array([193], dtype=np.int32)
+    got = O.bf16_value(O.decode_attention(bits(q), bits(k), bits(v), used, 128 ** -0.5))
+    mean = (64 * 2 + 64 * 6 + 65 * 20) / 193
+    assert (got == O.bf16_value(O.bf16_bits(np.float32(mean)))).all()
+    assert not np.allclose(got, (2 + 6 + 20 + 20) / 4)  # equal segment weights would be wrong
+    # one dominant block: all weight on the keys whose scores are largest
+    q.fill_(32)
+    k[:, :, :64], k[:, :, 64:128], k[:, :, 128:] = -32, 0, 32
+    got = O.bf16_value(O.decode_attention(bits(q), bits(k), bits(v), used, 128 ** -0.5))
+    assert (got == 20).all()
+    # no valid key -> zeros
+    got = O.decode_attention(bits(q), bits(k), bits(v), np.array([0], dtype=np.int32), 128 ** -0.5)
+    assert (got == 0).all()
+    # planted mistakes: the wrong kv head for a query head, or reading past `used`
+    g = gen(310)
+    q, k, v = normal((1, 8, 1, 128), g=g), normal((1, 2, 64, 128), g=g), normal((1, 2, 64, 128), g=g)
+    used = torch.tensor([40, 64], dtype=torch.int32)
+    good = O.decode_attention(bits(q), bits(k), bits(v), used.numpy(), 128 ** -0.5)
+    swapped = sdpa64(q, k.flip(1), v.flip(1), used.flip(0)).to(torch.bfloat16)
+    assert (O.ulp_distance(good, bits(swapped)) > 1).any()
+    past_end = sdpa64(q, k, v, torch.tensor([64, 64], dtype=torch.int32)).to(torch.bfloat16)
+    assert (O.ulp_distance(good, bits(past_end)) > 1).any()

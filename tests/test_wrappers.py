@@ -351,3 +351,51 @@ def test_skinny_marshalling():
     assert (name, m, k, n, splits) == ("qf_linear_partials", 5, 2560, 6144, p.shape[0])
     name, _, m, k, _, n = calls[1][:6]
     assert (name, m, k, n) == ("qf_linear_silu_mul", 5, 2560, 9728)
+
+
+def test_attention_partition_contract():
+    """The reference test's grid (tests/test_small_query_attention.py:217-230)."""
+    from starter_amd.kernels.small_query_attention import partition_keys
+    for heads in (1, 8, 24, 128, 512, 4096):
+        for capacity in (1, 63, 64, 65, 544, 2080, 8193, 262144):
+            for units in (1, 80, 114, 132, 144, 256):
+                splits, span = partition_keys(heads, capacity, units)
+                assert 1 <= splits <= 32 and span % 64 == 0
+                assert (splits - 1) * span < capacity <= splits * span
+    for args in ((0, 1, 1), (1, 0, 1), (1, 1, 0)):
+        with pytest.raises(ValueError):
+            partition_keys(*args)
+
+
+def test_attention_context_validation_and_marshalling():
+    from starter_amd.kernels import small_query_attention as sqa
+    props = mock.Mock(multi_processor_count=256)
+    fake = lambda shape, dtype, device: Fake(shape, dtype)  # noqa: E731
+    with mock.patch.object(torch.cuda, "get_device_properties", return_value=props), \
+            mock.patch.object(torch, "empty", side_effect=fake):
+        for bad in ((1, 34, 2, 13, "cuda"), (1, 8, 3, 13, "cuda"), (0, 8, 2, 13, "cuda"),
+                    (1, 8, 2, 13, "cpu")):
+            with pytest.raises(ValueError):
+                sqa.SmallQueryAttention(*bad)
+        plan = sqa.SmallQueryAttention(2, 8, 2, 257, "cuda:0")
+    assert (plan.groups, plan.virtual_heads) == (4, 4)
+    assert (plan.splits, plan.span) == sqa.partition_keys(4, 257, 256)
+    assert tuple(plan.partials.shape) == (4, plan.splits, 4, 128) and plan.partials.dtype == torch.float32
+    assert tuple(plan.stats.shape) == (4, plan.splits, 2, 4)
+    plan.partials.device = torch.device("cuda", 0)
+    q, k = Fake((2, 8, 1, 128)), Fake((2, 2, 257, 128))
+    used = Fake((4,), dtype=torch.int32)
+    with recorded() as calls, torch.no_grad():
+        out = plan.run(q, k, k, used, 0.25)
+    assert tuple(out.shape) == (2, 1, 8, 128)
+    name, *args = calls[0]
+    assert name == "qf_decode_attention"
+    assert args[4:11] == [2, 8, 2, 257, 0.25, plan.splits, plan.span]
+    for bad_args in ((q, k, k, Fake((4,), dtype=torch.int64), 0.25),
+                     (Fake((2, 8, 1, 128), dtype=torch.float32), k, k, used, 0.25),
+                     (q, k, k, used, float("nan")),
+                     (q, Fake((2, 2, 256, 128)), k, used, 0.25)):
+        with pytest.raises(ValueError), torch.no_grad():
+            plan.run(*bad_args)
+    with pytest.raises(ValueError):  # autograd enabled
+        plan.run(q, k, k, used, 0.25)
