@@ -345,6 +345,65 @@ def decode_attention_bench(device, replays: int = 20, calls: int = 24) -> dict:
     return out
 
 
+#: The engine contract's public workloads (batch, prompt tokens, output tokens).
+ENGINE_WORKLOADS = ((1, 512, 32), (4, 2048, 32), (16, 512, 128))
+
+
+def engine_decode(device, steps: int = 32) -> dict:
+    """End to end: starter_amd.engine.Engine on a randomly initialised
+    Qwen3-4B (the real architecture: 36 layers, hidden 2560, vocab 151936,
+    tied embedding) generating at the public workloads; the decode steps are
+    HIP-graph replays.  Reports decode tokens/s and the step's algorithmic
+    bytes (every weight once, the LM head, the K/V prefix read and the new
+    K/V rows written) against the HBM roofline."""
+    from transformers import Qwen3Config
+    from starter_amd.engine import Engine
+    cfg = Qwen3Config(vocab_size=V, hidden_size=H, intermediate_size=I, num_hidden_layers=36,
+                      num_attention_heads=NQ, num_key_value_heads=NK, head_dim=D,
+                      max_position_embeddings=40960, rope_theta=1_000_000, rms_norm_eps=1e-6,
+                      tie_word_embeddings=True)
+    engine = Engine(config=cfg, seed=0, device=device)
+    weight_bytes = sum(2 * t.numel() for layer in engine.layers
+                       for t in (layer.qkv, layer.o, layer.gate_up, layer.down))
+    weight_bytes += 2 * engine.lm_head.numel()
+    out = {"model": "Qwen3-4B architecture, random bf16 weights", "weight_bytes": weight_bytes}
+    g = torch.Generator().manual_seed(5)
+    for batch, length, new in ENGINE_WORKLOADS:
+        prompts = torch.randint(0, V, (batch, length), generator=g).tolist()
+        count = min(new, steps + 1)
+        gen = engine.generate(prompts, count)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        next(gen)                       # prefill (+ graph capture on first use)
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        t1 = time.perf_counter()
+        done = sum(1 for _ in gen)      # count - 1 decode steps, one host read each
+        t_decode = time.perf_counter() - t1
+        # second pass of the same shape: the captured graph is reused
+        gen = engine.generate(prompts, count)
+        next(gen)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        done = sum(1 for _ in gen)
+        t_decode = min(t_decode, time.perf_counter() - t1)
+        step_us = t_decode / done * 1e6
+        mid = length + done // 2        # average prefix length over the timed steps
+        kv = 36 * batch * NK * mid * D * 2 * 2 + 36 * batch * NK * D * 2 * 2
+        step_bytes = weight_bytes + kv + bf16_bytes(batch * H)
+        key = f"b{batch}_p{length}"
+        out[key] = {"decode_steps": done, "us_per_step": step_us,
+                    "tokens_per_s": batch / (step_us * 1e-6), "prefill_s": t_prefill,
+                    "step_bytes": step_bytes, "gbps": step_bytes / (step_us * 1e3),
+                    "frac": step_bytes / (step_us * 1e3) / PEAK_GBPS}
+        print(f"bench: engine {key:10s} decode {step_us:8.1f} us/step  {out[key]['tokens_per_s']:8.1f} tok/s "
+              f"({100 * out[key]['frac']:.1f}% of HBM roofline)  prefill {t_prefill:.2f} s",
+              file=sys.stderr, flush=True)
+    del engine
+    torch.cuda.empty_cache()
+    return out
+
+
 def graph_time_rotating(fn, calls: int, replays: int) -> float:
     """Median microseconds per call of ``fn(i)``, i = 0..calls-1, captured in one graph."""
     graph = capture(lambda: [fn(i) for i in range(calls)])
@@ -476,6 +535,8 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true", help="skip the decode configs")
     ap.add_argument("--no-proj", action="store_true",
                     help="skip the decode projections and decode attention")
+    ap.add_argument("--no-engine", action="store_true",
+                    help="skip the end-to-end Qwen3-4B decode through starter_amd.engine")
     ap.add_argument("--profile", type=int, default=0, metavar="N",
                     help="only run a calibration copy and N eager launches per prefill kernel "
                          "(for rocprofv3 --pmc), then exit")
@@ -530,6 +591,7 @@ def main() -> int:
                   flush=True)
         projections = {} if args.no_proj else decode_projections(device)
         attention = {} if args.no_proj else decode_attention_bench(device)
+    engine = {} if args.no_engine else engine_decode(device)
 
     dominant = max(KERNELS, key=lambda n: kernels[n]["us_per_call_mean"])
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": kernels[dominant]["gbps"],
@@ -561,6 +623,7 @@ def main() -> int:
         "decode": decode,
         "projections": projections,
         "attention": attention,
+        "engine": engine,
         "copy_gbps": copy_gbps,
     }
     if not args.no_cpu:

@@ -3,8 +3,8 @@
  * Qwen3-4B decode engine: residual-add + RMSNorm, per-head Q/K RMSNorm fused
  * with NeoX rotary embedding (three layouts), SiLU(gate)*up, the token
  * embedding gather, the rotary cos/sin table builder, the split-K decode
- * projections that feed the fused consumers, and grouped-query decode
- * attention over the K/V cache.
+ * projections that feed the fused consumers, grouped-query decode attention
+ * over the K/V cache, and the LM head fused with greedy token selection.
  *
  * Conventions shared by every entry point:
  *   - Tensors are plain device pointers.  "bf16" buffers hold IEEE bfloat16
@@ -231,6 +231,30 @@ int qf_decode_attention(const void* q, const void* k, const void* v, const int32
                         int64_t batch, int32_t q_heads, int32_t kv_heads, int64_t capacity,
                         float scale, int32_t splits, int64_t span, float* partials,
                         float* stats, void* out, void* stream);
+
+/*
+ * Candidate slots per row that qf_lm_head_argmax needs (vocab / 16), or a
+ * negative status when vocab is not a positive multiple of 16.
+ */
+int64_t qf_lm_head_blocks(int64_t vocab);
+
+/*
+ * LM head + greedy token selection (the final step of engine/decode.py:93,106
+ * and engine/decode_step.py:64, `logits.argmax(-1)` of F.linear(normed, W)):
+ *   logits[m, j] = bf16(x[m] . W[j])   (f32 accumulation on the matrix cores)
+ *   tokens[m]    = argmax_j logits[m, j], the LOWEST j among equal maxima
+ *                  (NaN counts as the maximum), as torch.argmax picks.
+ * x bf16 [rows, k], W bf16 [vocab, k] (the tied embedding), both contiguous
+ * and 16-byte aligned; 1 <= rows <= 64, k % 64 == 0, vocab % 16 == 0.
+ * candidates: scratch of rows * qf_lm_head_blocks(vocab) 8-byte slots
+ * (8-byte aligned; no initialisation needed).  tokens: int64 [rows].
+ * logits: optional bf16 [rows, vocab] copy of the logits (NULL to skip).
+ * Two launches (vocabulary tiles, then one workgroup per row).  No
+ * counterpart kernel in the reference, whose engine calls F.linear and
+ * torch.argmax (the fusion OPTIMIZATION_GUIDE.md:213 describes).
+ */
+int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const void* weight, int64_t vocab,
+                      void* candidates, int64_t* tokens, void* logits, void* stream);
 
 #ifdef __cplusplus
 }

@@ -41,6 +41,7 @@ _SIGNATURES = {
     "or_linear_silu_mul": ([_vp, _i64, _i64, _vp, _i64, _vp], None),
     "or_decode_attention": ([_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, ctypes.c_double, _vp, _vp],
                             None),
+    "or_lm_head_argmax": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp], None),
 }
 
 
@@ -264,3 +265,15 @@ def decode_attention(q, k, v, used, scale: float) -> np.ndarray:
     lib().or_decode_attention(_p(q), _p(k), _p(v), _p(used), batch, hq, hk, capacity, float(scale),
                               _p(scratch), _p(out))
     return out
+
+
+def lm_head_argmax(x, weight):
+    """engine/decode_step.py:64 + argmax: (tokens int64 [M], bf16 logits bits
+    [M, V]) with exactly rounded logits and first-maximum tie-breaking."""
+    x, weight = _u16(x), _u16(weight)
+    m, k = x.shape
+    vocab = weight.shape[0]
+    tokens = np.empty(m, dtype=np.int64)
+    logits = np.empty((m, vocab), dtype=np.uint16)
+    lib().or_lm_head_argmax(_p(x), m, k, _p(weight), vocab, _p(tokens), _p(logits))
+    return tokens, logits

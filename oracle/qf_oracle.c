@@ -41,6 +41,9 @@
  *                          head); known answers (zero queries -> mean of V,
  *                          one dominant key block -> its V); wrong head
  *                          mapping and reading past `used` are detected.
+ *   or_lm_head_argmax      logits bit-equal to torch float64 F.linear rounded
+ *                          to bf16; token = torch.argmax of them (first
+ *                          maximum) on integer inputs full of exact ties.
  *   or_linear_silu_mul     composition of exactly rounded projections with
  *                          or_silu_mul (bit-exact), torch float64 projections
  *                          + F.silu; skipping the projection rounding must
@@ -404,4 +407,29 @@ EXPORT void or_decode_attention(const uint16_t* q, const uint16_t* k, const uint
       }
       for (int d = 0; d < HEAD; ++d) o[d] = n ? or_bf16((float)(acc[d] / den)) : 0;
     }
+}
+
+/* ------------------------------------------------ LM head + token choice */
+
+/* engine/decode_step.py:64 and engine/decode.py:93: logits = bf16(x @ W^T)
+ * (exactly rounded here), token = argmax with the lowest index among equal
+ * maxima (torch.argmax returns the first maximum; NaN counts as maximal).
+ * x [m, k], W [vocab, k], tokens [m], logits [m, vocab] (may be NULL). */
+EXPORT void or_lm_head_argmax(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w,
+                              int64_t vocab, int64_t* tokens, uint16_t* logits) {
+  for (int64_t i = 0; i < m; ++i) {
+    float best = 0.0f;
+    int64_t besti = -1;
+    for (int64_t j = 0; j < vocab; ++j) {
+      const uint16_t b = or_bf16(dot_f32(x + i * k, w + j * k, 0, k));
+      if (logits) logits[i * vocab + j] = b;
+      const float v = or_f32(b);
+      const int vn = isnan(v), bn = besti >= 0 && isnan(best);
+      if (besti < 0 || (vn && !bn) || (!vn && !bn && v > best)) {
+        best = v;
+        besti = j;
+      }
+    }
+    tokens[i] = besti;
+  }
 }

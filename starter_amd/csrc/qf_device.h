@@ -142,6 +142,40 @@ __device__ __forceinline__ float inv_rms(double sum_sq, float n, float eps) {
   return 1.0f / sqrtf(var + eps);
 }
 
+// ---- f32 split-K partials ---------------------------------------------------
+
+// y[0..8) = f32 sum of `splits` partials of 8 consecutive columns, in split
+// order starting from 0: (((0 + p[0]) + p[1]) + ...), partial s at
+// p + s * stride.  Up to P partials are loaded before any of them is added,
+// so a call waits ceil(splits / P) memory latencies rather than `splits`.
+// Lanes with live == false load nothing and return zeros.
+template <int P>
+__device__ __forceinline__ void sum_partials8(const float* p, int64_t stride, int splits, bool live,
+                                              float* y) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = 0.0f;
+  for (int s0 = 0; s0 < splits; s0 += P) {
+    float4 lo[P], hi[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      lo[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      hi[i] = lo[i];
+      if (live && s0 + i < splits) {
+        const float4* q = reinterpret_cast<const float4*>(p + (int64_t)(s0 + i) * stride);
+        lo[i] = q[0];
+        hi[i] = q[1];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      if (s0 + i < splits) {
+        y[0] += lo[i].x; y[1] += lo[i].y; y[2] += lo[i].z; y[3] += lo[i].w;
+        y[4] += hi[i].x; y[5] += hi[i].y; y[6] += hi[i].z; y[7] += hi[i].w;
+      }
+    }
+  }
+}
+
 // ---- integer helpers --------------------------------------------------------
 
 // Unsigned 32-bit division by a run-time constant d >= 1 via a multiply-high

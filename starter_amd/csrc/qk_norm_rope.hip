@@ -179,16 +179,7 @@ __global__ __launch_bounds__(kBlock) void qkv_norm_rope_cache_kernel(QkvArgs a) 
               : zero4();
     unpack8(xv, x);
   } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = 0.0f;
-    const float* p = static_cast<const float*>(a.qkv) + off;
-    for (int s = 0; s < a.splits; ++s) {
-      const float4 p0 = live ? reinterpret_cast<const float4*>(p)[0] : make_float4(0, 0, 0, 0);
-      const float4 p1 = live ? reinterpret_cast<const float4*>(p)[1] : make_float4(0, 0, 0, 0);
-      x[0] += p0.x; x[1] += p0.y; x[2] += p0.z; x[3] += p0.w;
-      x[4] += p1.x; x[5] += p1.y; x[6] += p1.z; x[7] += p1.w;
-      p += a.split_stride;
-    }
+    sum_partials8<16>(static_cast<const float*>(a.qkv) + off, a.split_stride, a.splits, live, x);
     xv = pack8(x);  // one rounding of the f32 sum
     unpack8(xv, x);
   }

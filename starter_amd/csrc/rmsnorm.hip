@@ -13,7 +13,8 @@
 // bytes.  The row stays in registers between the reduction and the output, so
 // every input byte is read once and every output byte written once.  The sum
 // of squares is reduced in f64 with DPP inside 16-lane rows and ds_bpermute
-// across them; no LDS allocation and no barrier.
+// across them; no LDS allocation and no barrier.  Split-K partials (decode)
+// take rms_partials_kernel, one workgroup per row.
 #include "qf_device.h"
 
 namespace qf {
@@ -193,6 +194,57 @@ int launch_vec(const RmsArgs& a, hipStream_t s) {
   return launch_rows<LPR, VPL, MODE, 1, true>(a, s);
 }
 
+// Residual add of f32 split-K partials + RMSNorm for decode-size calls: one
+// workgroup per row, one thread per 16-byte vector of the row (cols / 8 <= 1024
+// threads), up to P partials of a vector loaded before any is added (split
+// order kept), the f64 sum of squares reduced across waves through LDS in
+// wave order (exact, so order-free).  A wave-per-row kernel would walk the
+// splits one memory latency at a time for each of its vectors.
+template <int P, int MAXT>
+__global__ __launch_bounds__(MAXT) void rms_partials_kernel(RmsArgs a) {
+  __shared__ double wave_sums[MAXT / kWave];
+  __shared__ double row_sum;
+  const int64_t row = blockIdx.x;
+  const int v = threadIdx.x;
+  const bool on = v < a.nvec;
+  const int vi = on ? v : 0;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const uint4 xv = on ? load16<false>(reinterpret_cast<const uint4*>(a.x + row * a.cols) + vi)
+                      : make_uint4(0, 0, 0, 0);
+  float y[8], t[8];
+  sum_partials8<P>(static_cast<const float*>(a.branch) + row * a.cols + (int64_t)vi * 8,
+                   a.split_stride, a.splits, on, y);
+  round8(y);
+  unpack8(xv, t);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) t[j] += y[j];
+  const uint4 tv = pack8(t);
+  unpack8(tv, t);
+  if (on) store16<false>(reinterpret_cast<uint4*>(a.total + row * a.cols) + v, tv);
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += (double)(t[j] * t[j]);
+  ss = group_sum_f64<kWave>(ss);
+  if (lane == 0) wave_sums[wave] = ss;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double tot = 0.0;
+    for (int w = 0; w < (int)(blockDim.x / kWave); ++w) tot += wave_sums[w];
+    row_sum = tot;
+  }
+  __syncthreads();
+  if (!on) return;
+  const float inv = inv_rms(row_sum, (float)a.cols, a.eps);
+  float n[8], w[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) n[j] = t[j] * inv;
+  round8(n);
+  unpack8(reinterpret_cast<const uint4*>(a.w)[v], w);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) n[j] *= w[j];
+  store16<false>(reinterpret_cast<uint4*>(a.out + row * a.cols) + v, pack8(n));
+}
+
 template <int MODE>
 int dispatch(RmsArgs a, bool vec_ok, hipStream_t s) {
   constexpr bool ADD = MODE != 0;
@@ -200,6 +252,16 @@ int dispatch(RmsArgs a, bool vec_ok, hipStream_t s) {
   if (vec_ok) {
     a.nvec = (int32_t)(a.cols / 8);
     const int nv = a.nvec;
+    if (MODE == 2 && nv <= 1024 && a.rows <= (int64_t)UINT32_MAX) {
+      // 16 partials in flight per thread up to 4096 columns (512 threads);
+      // 8 beyond, where 1024 threads leave 128 registers each.
+      const int threads = (nv + kWave - 1) / kWave * kWave;
+      if (nv <= 512)
+        hipLaunchKernelGGL((rms_partials_kernel<16, 512>), dim3((unsigned)a.rows), dim3(threads), 0, s, a);
+      else
+        hipLaunchKernelGGL((rms_partials_kernel<8, 1024>), dim3((unsigned)a.rows), dim3(threads), 0, s, a);
+      return launch_status();
+    }
     if (nv <= 8) return launch_vec<8, 1, MODE>(a, s);
     if (nv <= 16) return launch_vec<16, 1, MODE>(a, s);
     if (nv <= 32) return launch_vec<32, 1, MODE>(a, s);

@@ -60,11 +60,24 @@ constexpr int kWaves = kBlock / kWave;
 constexpr int kMaxRows = 64;
 constexpr int kColAlign = 32;  // N granularity of the shape rule
 
+// Epilogues.
+constexpr int kEpiPartials = 0;  // f32 split-K partials [S, M, N]
+constexpr int kEpiSiluMul = 1;   // packed gate/up -> bf16 silu(gate) * up [M, N]
+constexpr int kEpiArgmax = 2;    // bf16 logits (optional) + per-workgroup argmax candidates
+
+// Is (v, i) ahead of (bv, bi) in argmax order: larger value, NaN above
+// everything, the lower index on equal values (torch.argmax's first maximum)?
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
 struct SkinnyArgs {
   const uint16_t* x;   // [m, k]
   const uint16_t* w;   // [n, k], or [2n, k] gate rows then up rows
-  float* partials;     // [splits, m, n]
-  uint16_t* out;       // [m, n]
+  float* partials;     // [splits, m, n]; argmax: (value, index) pairs [m, workgroups]
+  uint16_t* out;       // [m, n] (argmax: optional bf16 logits, may be null)
   int64_t k;
   int32_t m;
   int32_t n;           // output columns
@@ -95,8 +108,9 @@ constexpr int kRowsPerLoad = kWave * 16 / (kChunk * 2);  // 8 rows x 128 B per l
 // the chunks; D chunks in flight per wave; NTL = nontemporal weight loads.
 // Waves of different groups read the same x chunk at about the same time,
 // so x is fetched from L2 once per workgroup rather than once per wave.
-template <int MT, int NT, int WK, int D, bool PAIRS, bool NTL, bool XT>
+template <int MT, int NT, int WK, int D, int EPI, bool NTL, bool XT>
 __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
+  constexpr bool PAIRS = EPI == kEpiSiluMul;
   static_assert(kWaves % WK == 0, "wave split");
   constexpr int WN = kWaves / WK;
   constexpr int kCols = PAIRS ? NT / 2 : NT;  // output n-tiles per wave
@@ -259,6 +273,48 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
           acc[t][mt] += handoff[(wn * (WK - 1) + w) * kPer + (t * MT + mt) * kWave + lane];
   }
 
+  if constexpr (EPI == kEpiArgmax) {
+    // bf16 logits of this workgroup's 16*NT columns; per row the largest,
+    // lowest column on ties (NaN counts as largest), reduced over the four
+    // lanes that hold a row (all lanes take part in the shuffles).
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = kTile * mt + r;
+      const bool row_ok = live && m < a.m;
+      float best = -__builtin_inff();
+      int besti = INT32_MAX;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = from_bf16(to_bf16(acc[t][mt][i]));
+          const int col = col0 + kTile * t + 4 * g + i;
+          if (better(v[i], col, best, besti)) {
+            best = v[i];
+            besti = col;
+          }
+        }
+        if (row_ok && a.out)
+          *reinterpret_cast<uint2*>(a.out + (int64_t)m * a.n + col0 + kTile * t + 4 * g) =
+              make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+      }
+#pragma unroll
+      for (int mask = 16; mask <= 32; mask *= 2) {
+        const float ov = __shfl_xor(best, mask);
+        const int oi = __shfl_xor(besti, mask);
+        if (better(ov, oi, best, besti)) {
+          best = ov;
+          besti = oi;
+        }
+      }
+      if (row_ok && g == 0) {
+        uint2* cand = reinterpret_cast<uint2*>(a.partials) + (int64_t)m * gridDim.x + blockIdx.x;
+        *cand = make_uint2(__float_as_uint(best), (uint32_t)besti);
+      }
+    }
+    return;
+  }
   if (!live) return;
   if constexpr (!PAIRS) {
 #pragma unroll
@@ -316,11 +372,11 @@ int plan_splits(int64_t rows, int64_t k, int64_t n) {
   return (int)s;
 }
 
-template <int MT, int NT, int WK, int D, bool PAIRS, bool NTL, bool XT>
+template <int MT, int NT, int WK, int D, int EPI, bool NTL, bool XT>
 int launch(const SkinnyArgs& a, int splits, hipStream_t s) {
-  constexpr int kColsPerBlock = kTile * (PAIRS ? NT / 2 : NT) * (kWaves / WK);
+  constexpr int kColsPerBlock = kTile * (EPI == kEpiSiluMul ? NT / 2 : NT) * (kWaves / WK);
   const int64_t grid_x = (a.n + kColsPerBlock - 1) / kColsPerBlock;
-  hipLaunchKernelGGL((skinny_kernel<MT, NT, WK, D, PAIRS, NTL, XT>),
+  hipLaunchKernelGGL((skinny_kernel<MT, NT, WK, D, EPI, NTL, XT>),
                      dim3((unsigned)grid_x, (unsigned)splits), dim3(kBlock), 0, s, a);
   return launch_status();
 }
@@ -332,23 +388,76 @@ int launch(const SkinnyArgs& a, int splits, hipStream_t s) {
 int dispatch_partials(const SkinnyArgs& a, int splits, hipStream_t s) {
   switch ((a.m + kTile - 1) / kTile) {
     case 1:
-      if (a.m <= 4) return launch<1, 1, 4, 2, false, true, false>(a, splits, s);
-      if (a.n / kTile >= 256) return launch<1, 2, 4, 2, false, true, true>(a, splits, s);
-      return launch<1, 1, 4, 2, false, true, true>(a, splits, s);
-    case 2: return launch<2, 2, 4, 2, false, true, true>(a, splits, s);
-    case 3: return launch<3, 2, 4, 2, false, true, true>(a, splits, s);
-    default: return launch<4, 2, 4, 2, false, true, true>(a, splits, s);
+      if (a.m <= 4) return launch<1, 1, 4, 2, kEpiPartials, true, false>(a, splits, s);
+      if (a.n / kTile >= 256) return launch<1, 2, 4, 2, kEpiPartials, true, true>(a, splits, s);
+      return launch<1, 1, 4, 2, kEpiPartials, true, true>(a, splits, s);
+    case 2: return launch<2, 2, 4, 2, kEpiPartials, true, true>(a, splits, s);
+    case 3: return launch<3, 2, 4, 2, kEpiPartials, true, true>(a, splits, s);
+    default: return launch<4, 2, 4, 2, kEpiPartials, true, true>(a, splits, s);
   }
 }
 
 int dispatch_silu(const SkinnyArgs& a, hipStream_t s) {
   switch ((a.m + kTile - 1) / kTile) {
     case 1:
-      if (a.m <= 4) return launch<1, 2, 4, 4, true, true, false>(a, 1, s);
-      return launch<1, 2, 4, 4, true, true, true>(a, 1, s);
-    case 2: return launch<2, 2, 4, 2, true, true, true>(a, 1, s);
-    case 3: return launch<3, 2, 4, 2, true, true, true>(a, 1, s);
-    default: return launch<4, 2, 4, 2, true, true, true>(a, 1, s);
+      if (a.m <= 4) return launch<1, 2, 4, 4, kEpiSiluMul, true, false>(a, 1, s);
+      return launch<1, 2, 4, 4, kEpiSiluMul, true, true>(a, 1, s);
+    case 2: return launch<2, 2, 4, 2, kEpiSiluMul, true, true>(a, 1, s);
+    case 3: return launch<3, 2, 4, 2, kEpiSiluMul, true, true>(a, 1, s);
+    default: return launch<4, 2, 4, 2, kEpiSiluMul, true, true>(a, 1, s);
+  }
+}
+
+// Final argmax over a row's workgroup candidates: one workgroup per row.
+__global__ __launch_bounds__(kBlock) void argmax_finalize_kernel(const uint2* cand, int64_t blocks,
+                                                                int64_t* tokens) {
+  __shared__ float wv[kWaves];
+  __shared__ int wi[kWaves];
+  const int64_t row = blockIdx.x;
+  float best = -__builtin_inff();
+  int besti = INT32_MAX;
+  for (int64_t j = threadIdx.x; j < blocks; j += kBlock) {
+    const uint2 c = cand[row * blocks + j];
+    const float v = __uint_as_float(c.x);
+    const int i = (int)c.y;
+    if (better(v, i, best, besti)) {
+      best = v;
+      besti = i;
+    }
+  }
+#pragma unroll
+  for (int mask = 1; mask < kWave; mask *= 2) {
+    const float ov = __shfl_xor(best, mask);
+    const int oi = __shfl_xor(besti, mask);
+    if (better(ov, oi, best, besti)) {
+      best = ov;
+      besti = oi;
+    }
+  }
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  if (lane == 0) {
+    wv[wave] = best;
+    wi[wave] = besti;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWaves; ++w)
+      if (better(wv[w], wi[w], best, besti)) {
+        best = wv[w];
+        besti = wi[w];
+      }
+    tokens[row] = besti;
+  }
+}
+
+int dispatch_argmax(const SkinnyArgs& a, hipStream_t s) {
+  switch ((a.m + kTile - 1) / kTile) {
+    case 1:
+      if (a.m <= 4) return launch<1, 1, 4, 2, kEpiArgmax, true, false>(a, 1, s);
+      return launch<1, 1, 4, 2, kEpiArgmax, true, true>(a, 1, s);
+    case 2: return launch<2, 1, 4, 2, kEpiArgmax, true, true>(a, 1, s);
+    case 3: return launch<3, 1, 4, 2, kEpiArgmax, true, true>(a, 1, s);
+    default: return launch<4, 1, 4, 2, kEpiArgmax, true, true>(a, 1, s);
   }
 }
 
@@ -356,6 +465,37 @@ int dispatch_silu(const SkinnyArgs& a, hipStream_t s) {
 }  // namespace qf
 
 using namespace qf;
+
+extern "C" int64_t qf_lm_head_blocks(int64_t vocab) {
+  return vocab > 0 && vocab % kTile == 0 ? vocab / kTile : QF_E_SHAPE;
+}
+
+extern "C" int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const void* weight,
+                                 int64_t vocab, void* candidates, int64_t* tokens, void* logits,
+                                 void* stream) {
+  if (rows < 1 || rows > kMaxRows || k <= 0 || k % kChunk != 0 || k > (int64_t)INT32_MAX ||
+      vocab <= 0 || vocab % kTile != 0 || vocab > (int64_t)INT32_MAX / 2)
+    return QF_E_SHAPE;
+  if (!x || !weight || !candidates || !tokens) return QF_E_ARG;
+  if (!aligned16(x) || !aligned16(weight) || (reinterpret_cast<uintptr_t>(candidates) & 7u) != 0 ||
+      (reinterpret_cast<uintptr_t>(logits) & 7u) != 0)
+    return QF_E_ALIGN;
+  SkinnyArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(weight);
+  a.partials = static_cast<float*>(candidates);
+  a.out = static_cast<uint16_t*>(logits);
+  a.k = k;
+  a.m = (int32_t)rows;
+  a.n = (int32_t)vocab;
+  a.chunks = (int32_t)(k / kChunk);
+  hipStream_t s = as_stream(stream);
+  const int st = dispatch_argmax(a, s);
+  if (st != QF_OK) return st;
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)rows), dim3(kBlock), 0, s,
+                     static_cast<const uint2*>(candidates), vocab / kTile, tokens);
+  return launch_status();
+}
 
 extern "C" int qf_linear_splits(int64_t rows, int64_t k, int64_t n) {
   const int st = shape_status(rows, k, n);

@@ -1,0 +1,272 @@
+"""Engine-shaped greedy generation over the fused HIP kernels.
+
+Same interface as the reference's ``engine/engine.py`` (jadenpxrk/starter,
+README.md:49-66): ``Engine(model_path)`` loads a Qwen3 checkpoint and
+``generate(input_ids, max_new_tokens)`` yields one ``list[int]`` (a token id
+per sequence) per output step, exactly ``max_new_tokens`` times.  Built from
+scratch on this package's kernels to show them composing inside the loop the
+reference runs:
+
+* prefill (``engine/prefill.py:26-66``): embedding gather, RMSNorm, packed QKV
+  projection (hipBLASLt), ``prefill_qkv`` (Q/K norm + RoPE + K/V cache write),
+  causal attention, and the residual-add + RMSNorm / SiLU * up fusions;
+* decode (``engine/decode_step.py:33-64``): the split-K projections whose f32
+  partials feed ``qkv_norm_rope_cache`` and ``add_rms_norm``, the fused
+  gate/up projection with its SiLU epilogue, split-KV decode attention, and
+  the LM head fused with the greedy token choice; the whole step is captured once per
+  (batch, capacity) in a HIP graph and replayed with the position and cache
+  lengths advanced on the device.
+
+Weights come from transformers' ``Qwen3ForCausalLM`` - from a local
+checkpoint directory, or randomly initialised from a config - and are packed
+once (Q|K|V and gate|up rows, as ``engine/engine.py:39-47`` packs them).
+Prefill attention runs in float32 with explicit matmuls; everything else is
+bf16.  There is no CPU path: the engine needs a GPU and the HIP library.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch.nn import functional as F
+
+from .kernels.decode_fused import add_rms_norm, qkv_norm_rope_cache, silu_mul
+from .kernels.embedding import embedding
+from .kernels import lm_head as _lm_head
+from .kernels.prefill import prefill_qkv
+from .kernels.rmsnorm import rms_norm
+from .kernels.rotary import rope_tables
+from .kernels.skinny_gemm import linear_partials, linear_silu_mul, supports
+from .kernels.small_query_attention import SmallQueryAttention
+
+HEAD = 128
+
+
+@dataclass
+class PackedLayer:
+    """One decoder layer's weights in the layout the fused path reads."""
+    qkv: torch.Tensor        # [(Hq + 2 Hkv) * 128, H]: q rows, k rows, v rows
+    o: torch.Tensor          # [H, Hq * 128]
+    gate_up: torch.Tensor    # [2 I, H]: gate rows, up rows
+    down: torch.Tensor       # [H, I]
+    ln_in: torch.Tensor
+    ln_post: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+    eps_in: float
+    eps_post: float
+    eps_q: float
+    eps_k: float
+
+
+def pack_layer(layer) -> PackedLayer:
+    """Pack a transformers ``Qwen3DecoderLayer`` (any device / dtype kept)."""
+    attn, mlp = layer.self_attn, layer.mlp
+    return PackedLayer(
+        qkv=torch.cat([attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight]).contiguous(),
+        o=attn.o_proj.weight.contiguous(),
+        gate_up=torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight]).contiguous(),
+        down=mlp.down_proj.weight.contiguous(),
+        ln_in=layer.input_layernorm.weight.contiguous(),
+        ln_post=layer.post_attention_layernorm.weight.contiguous(),
+        q_norm=attn.q_norm.weight.contiguous(),
+        k_norm=attn.k_norm.weight.contiguous(),
+        eps_in=float(layer.input_layernorm.variance_epsilon),
+        eps_post=float(layer.post_attention_layernorm.variance_epsilon),
+        eps_q=float(attn.q_norm.variance_epsilon),
+        eps_k=float(attn.k_norm.variance_epsilon),
+    )
+
+
+class _State:
+    """Caches, rotary tables and graph buffers for one (batch, capacity)."""
+
+    def __init__(self, engine: "Engine", batch: int, capacity: int):
+        dev = engine.device
+        self.batch, self.capacity = batch, capacity
+        shape = (batch, engine.kv_heads, capacity, HEAD)
+        self.keys = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in engine.layers]
+        self.values = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in engine.layers]
+        self.cos, self.sin = rope_tables(engine.inv_freq, capacity, device=dev)
+        self.attention = SmallQueryAttention(batch, engine.q_heads, engine.kv_heads, capacity, dev)
+        self.tokens = torch.zeros(batch, dtype=torch.int64, device=dev)
+        self.position = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.used = torch.zeros(batch * engine.kv_heads, dtype=torch.int32, device=dev)
+        self.graph = None
+        self.logits = None
+
+
+class Engine:
+    """Greedy Qwen3 generation on the fused gfx950 kernels (see module doc)."""
+
+    def __init__(self, model_path: str | None = None, *, config=None, seed: int = 0,
+                 device: str | torch.device = "cuda", use_graphs: bool = True):
+        from transformers import Qwen3ForCausalLM
+        self.device = torch.device(device)
+        if self.device.type != "cuda" or not torch.cuda.is_available():
+            raise RuntimeError("Engine needs a GPU: the fused kernels have no CPU path")
+        if model_path is not None:
+            model = Qwen3ForCausalLM.from_pretrained(model_path, torch_dtype=torch.bfloat16,
+                                                     local_files_only=True)
+        elif config is not None:
+            torch.manual_seed(seed)
+            with torch.device(self.device):  # initialise on the GPU (seconds for 4B params)
+                model = Qwen3ForCausalLM(config).to(torch.bfloat16)
+        else:
+            raise ValueError("give a local checkpoint directory or a Qwen3Config")
+        model = model.to(self.device).eval()
+        cfg = model.config
+        self.config = cfg
+        self.model = model
+        self.q_heads, self.kv_heads = cfg.num_attention_heads, cfg.num_key_value_heads
+        width = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        if width != HEAD:
+            raise ValueError(f"the fused Q/K kernels need head_dim {HEAD}, not {width}")
+        self.scale = model.model.layers[0].self_attn.scaling
+        with torch.no_grad():
+            self.layers = [pack_layer(layer) for layer in model.model.layers]
+        self.embed = model.model.embed_tokens.weight
+        self.final_norm = model.model.norm.weight
+        self.final_eps = float(model.model.norm.variance_epsilon)
+        self.lm_head = model.lm_head.weight
+        self.inv_freq = model.model.rotary_emb.inv_freq.float()
+        self.use_graphs = use_graphs
+        self._states: dict[tuple[int, int], _State] = {}
+        self.last_logits = None
+
+    # ------------------------------------------------------------ helpers
+
+    @staticmethod
+    def _project(x, weight):
+        """x @ weight.T as f32 split-K partials when decode-sized, else bf16."""
+        return linear_partials(x, weight) if supports(x, weight) else F.linear(x, weight)
+
+    @staticmethod
+    def _mlp_hidden(normed, gate_up):
+        if supports(normed, gate_up, pairs=True):
+            return linear_silu_mul(normed, gate_up)
+        return silu_mul(F.linear(normed, gate_up))
+
+    def _select(self, normed, tokens):
+        """LM head + greedy choice: writes the tokens, returns the bf16 logits."""
+        if _lm_head.supports(normed, self.lm_head):
+            return _lm_head.lm_head_argmax(normed, self.lm_head, logits=True, tokens=tokens)[1]
+        logits = F.linear(normed, self.lm_head)
+        tokens.copy_(logits.argmax(-1))
+        return logits
+
+    def _next_norm(self, index):
+        if index + 1 < len(self.layers):
+            nxt = self.layers[index + 1]
+            return nxt.ln_in, nxt.eps_in
+        return self.final_norm, self.final_eps
+
+    def _state(self, batch, capacity) -> _State:
+        key = (batch, capacity)
+        if key not in self._states:
+            self._states[key] = _State(self, batch, capacity)
+        return self._states[key]
+
+    # ------------------------------------------------------------ prefill
+
+    def _prefill_attention(self, q, keys, values, length):
+        """Causal GQA attention over the prompt in float32: q [B, T, Hq, 128]."""
+        batch = q.shape[0]
+        groups = self.q_heads // self.kv_heads
+        qf = q.float().view(batch, length, self.kv_heads, groups, HEAD).permute(0, 2, 3, 1, 4)
+        k = keys[:, :, :length].float().unsqueeze(2)          # [B, Hkv, 1, T, D]
+        v = values[:, :, :length].float().unsqueeze(2)
+        scores = torch.matmul(qf, k.transpose(-1, -2).contiguous()) * self.scale
+        causal = torch.ones(length, length, dtype=torch.bool, device=q.device).tril()
+        scores = scores.masked_fill(~causal, float("-inf"))
+        out = torch.matmul(torch.softmax(scores, dim=-1), v)   # [B, Hkv, G, T, D]
+        return out.permute(0, 3, 1, 2, 4).reshape(batch * length, self.q_heads * HEAD).to(torch.bfloat16)
+
+    def _prefill(self, st: _State, ids: torch.Tensor):
+        batch, length = ids.shape
+        x = embedding(ids.reshape(-1), self.embed)
+        first = self.layers[0]
+        normed = rms_norm(x, first.ln_in, first.eps_in)
+        for index, layer in enumerate(self.layers):
+            q = prefill_qkv(F.linear(normed, layer.qkv), layer.q_norm, layer.k_norm, layer.eps_q,
+                            layer.eps_k, st.cos, st.sin, st.keys[index], st.values[index], length)
+            attended = self._prefill_attention(q, st.keys[index], st.values[index], length)
+            x, normed = add_rms_norm(x, F.linear(attended, layer.o), layer.ln_post, layer.eps_post)
+            hidden = silu_mul(F.linear(normed, layer.gate_up))
+            weight, eps = self._next_norm(index)
+            x, normed = add_rms_norm(x, F.linear(hidden, layer.down), weight, eps)
+        last = normed.view(batch, length, -1)[:, -1].contiguous()
+        return self._select(last, st.tokens)
+
+    # ------------------------------------------------------------- decode
+
+    def _decode_step(self, st: _State):
+        """One token per sequence at slot ``st.position``; advances the
+        position and lengths on the device (capturable)."""
+        batch = st.batch
+        x = embedding(st.tokens, self.embed)
+        first = self.layers[0]
+        normed = rms_norm(x, first.ln_in, first.eps_in)
+        for index, layer in enumerate(self.layers):
+            q = qkv_norm_rope_cache(self._project(normed, layer.qkv), layer.q_norm, layer.k_norm,
+                                    layer.eps_q, layer.eps_k, st.cos, st.sin, st.position,
+                                    st.keys[index], st.values[index])
+            attended = st.attention.run(q, st.keys[index], st.values[index], st.used, self.scale)
+            x, normed = add_rms_norm(x, self._project(attended.view(batch, -1), layer.o),
+                                     layer.ln_post, layer.eps_post)
+            hidden = self._mlp_hidden(normed, layer.gate_up)
+            weight, eps = self._next_norm(index)
+            x, normed = add_rms_norm(x, self._project(hidden, layer.down), weight, eps)
+        logits = self._select(normed, st.tokens)
+        st.position.add_(1)
+        st.used.add_(1)
+        return logits
+
+    def _capture(self, st: _State):
+        """Capture the decode step into a HIP graph.  The warm-up runs repeat
+        the first step (same token, same slot), so they leave the caches as
+        the first replay does; the buffers are restored before replaying."""
+        saved = (st.tokens.clone(), st.position.clone(), st.used.clone())
+        stream = torch.cuda.Stream(self.device)
+        stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(stream):
+            for _ in range(2):
+                st.tokens.copy_(saved[0]); st.position.copy_(saved[1]); st.used.copy_(saved[2])
+                self._decode_step(st)
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        st.tokens.copy_(saved[0]); st.position.copy_(saved[1]); st.used.copy_(saved[2])
+        with torch.cuda.graph(graph, stream=stream):
+            st.logits = self._decode_step(st)
+        st.tokens.copy_(saved[0]); st.position.copy_(saved[1]); st.used.copy_(saved[2])
+        st.graph = graph
+
+    # ------------------------------------------------------------ generate
+
+    @torch.inference_mode()
+    def generate(self, input_ids: list[list[int]], max_new_tokens: int):
+        """Greedy continuation; yields one list[int] per step, max_new_tokens times."""
+        if max_new_tokens < 1 or not input_ids:
+            raise ValueError("need at least one sequence and one new token")
+        length = len(input_ids[0])
+        if length < 1 or any(len(row) != length for row in input_ids):
+            raise ValueError("every sequence in input_ids must have the same non-zero length")
+        batch = len(input_ids)
+        st = self._state(batch, length + max_new_tokens)
+        ids = torch.tensor(input_ids, dtype=torch.int64, device=self.device)
+        self.last_logits = self._prefill(st, ids)
+        yield st.tokens.tolist()
+        if max_new_tokens == 1:
+            return
+        st.position.fill_(length)
+        st.used.fill_(length + 1)
+        if self.use_graphs and st.graph is None:
+            self._capture(st)
+        for _ in range(max_new_tokens - 1):
+            if self.use_graphs:
+                st.graph.replay()
+                self.last_logits = st.logits
+            else:
+                self.last_logits = self._decode_step(st)
+            yield st.tokens.tolist()

@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 15
+    assert len(names) == 17
 
 
 def test_library_exports_every_symbol():
@@ -80,6 +80,12 @@ def test_host_side_argument_errors_launch_nothing():
     assert lib.qf_linear_partials(bogus, 65, 2560, bogus, 6144, 1, bogus, None) == -2
     assert lib.qf_linear_silu_mul(bogus, 4, 2560, bogus, 9728, bogus + 4, None) == -3
     assert lib.qf_linear_silu_mul(bogus, 4, 2560, bogus, 9720, bogus, None) == -2
+    # LM head: shape rule and alignment
+    assert lib.qf_lm_head_blocks(151936) == 9496 and lib.qf_lm_head_blocks(100) == -2
+    assert lib.qf_lm_head_argmax(bogus, 65, 2560, bogus, 151936, bogus, bogus, None, None) == -2
+    assert lib.qf_lm_head_argmax(bogus, 1, 2560, bogus, 151930, bogus, bogus, None, None) == -2
+    assert lib.qf_lm_head_argmax(bogus, 1, 2560, bogus, 151936, None, bogus, None, None) == -1
+    assert lib.qf_lm_head_argmax(bogus + 8, 1, 2560, bogus, 151936, bogus, bogus, None, None) == -3
     # decode attention: group size, split plan, scale, alignment
     split, span = ctypes.c_int32(), ctypes.c_int64()
     assert lib.qf_attention_partition(0, 64, 256, ctypes.byref(split), ctypes.byref(span)) == -1

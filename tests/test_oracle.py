@@ -548,3 +548,26 @@ def test_decode_attention_known_answers_and_planted_mistakes():
     assert (O.ulp_distance(good, bits(swapped)) > 1).any()
     past_end = sdpa64(q, k, v, torch.tensor([64, 64], dtype=torch.int32)).to(torch.bfloat16)
     assert (O.ulp_distance(good, bits(past_end)) > 1).any()
+
+
+# --------------------------------------------------- LM head + token choice
+
+def test_lm_head_argmax_matches_torch_and_breaks_ties_low():
+    g = gen(500)
+    x, w = normal((3, 256), g=g), normal((1024, 256), 0.0, 0.1, g)
+    tokens, logits = O.lm_head_argmax(bits(x), bits(w))
+    expected = F.linear(x.double(), w.double()).float().to(torch.bfloat16)
+    np.testing.assert_array_equal(logits, bits(expected))
+    np.testing.assert_array_equal(tokens, expected.argmax(-1).numpy())
+    # integer inputs: many exactly equal logits; the first maximum wins
+    xi = torch.zeros(5, 64, dtype=torch.bfloat16)
+    xi[:, 0] = 1
+    xi[:, 1:3] = torch.randint(0, 2, (5, 2), generator=g).to(torch.bfloat16)
+    wi = torch.randint(-1, 2, (512, 64), generator=g).to(torch.bfloat16)
+    tokens, logits = O.lm_head_argmax(bits(xi), bits(wi))
+    exact = (xi.to(torch.int64) @ wi.to(torch.int64).T)
+    assert all(int((exact[r] == exact[r].max()).sum()) > 1 for r in range(5))  # ties present
+    np.testing.assert_array_equal(tokens, np.argmax(exact.numpy(), axis=1))    # numpy: first maximum
+    # planted mistake: the last maximum instead of the first
+    last = exact.shape[1] - 1 - np.argmax(exact.numpy()[:, ::-1], axis=1)
+    assert (tokens != last).any()

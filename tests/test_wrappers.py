@@ -399,3 +399,20 @@ def test_attention_context_validation_and_marshalling():
             plan.run(*bad_args)
     with pytest.raises(ValueError):  # autograd enabled
         plan.run(q, k, k, used, 0.25)
+
+
+def test_lm_head_rule_and_marshalling():
+    from starter_amd.kernels import lm_head
+    x, w = Fake((4, 2560)), Fake((151936, 2560))
+    assert lm_head.supports(x, w)
+    for bad_x, bad_w in ((Fake((65, 2560)), w), (x, Fake((151930, 2560))), (Fake((4, 2570)), Fake((16, 2570))),
+                         (Fake((4, 2560), cuda=False), Fake((16, 2560), cuda=False))):
+        assert not lm_head.supports(bad_x, bad_w)
+    with pytest.raises(ValueError):
+        lm_head.lm_head_argmax(Fake((4, 2560), dtype=torch.float32), w)
+    with recorded() as calls:
+        tokens, logits = lm_head.lm_head_argmax(x, w, logits=True)
+    assert tuple(tokens.shape) == (4,) and tokens.dtype == torch.int64
+    assert tuple(logits.shape) == (4, 151936)
+    name, _, rows, k, _, vocab = calls[0][:6]
+    assert (name, rows, k, vocab) == ("qf_lm_head_argmax", 4, 2560, 151936)
