@@ -32,8 +32,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kD = 128;
 constexpr int kKeysPerWave = 4;                       // one 1 KiB load = 4 key rows
-constexpr int kWavesA = kBlock / kWave;
-constexpr int kKeysPerIter = kKeysPerWave * kWavesA;  // 16 keys per workgroup step
+constexpr int kSpanAlign = 16;                        // segment lengths are multiples of 16
 constexpr int kMaxGroups = 16;
 constexpr int kMaxSplits = 32;
 constexpr float kNegInf = -__builtin_inff();
@@ -112,8 +111,10 @@ __device__ __forceinline__ void merge_lanes(State<GT>& s, int mask) {
 // blocks (4 keys per wave each) in flight.  With one segment the workgroup
 // writes the output; otherwise it writes its f32 partials and statistics for
 // attn_merge_kernel.
-template <int GT, int U>
-__global__ __launch_bounds__(kBlock) void attn_kernel(AttnArgs a) {
+template <int GT, int U, int W>
+__global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
+  constexpr int kWavesA = W;
+  constexpr int kKeysPerIter = kKeysPerWave * W;  // keys per workgroup step
   __shared__ float xm[kWavesA - 1][GT], xl[kWavesA - 1][GT];
   __shared__ float xacc[kWavesA - 1][GT][kD];
   const int vh = blockIdx.x;
@@ -276,7 +277,9 @@ __global__ __launch_bounds__(kBlock) void attn_kernel(AttnArgs a) {
 }
 
 // One 16-lane group per query row (4 rows per wave): weights 2^(m_s - M)
-// for segments with a positive denominator, summed in segment order.
+// for segments with a positive denominator, summed in segment order.  All
+// statistics, then the partials in groups of 8 segments, are loaded before
+// they are combined, so the kernel waits a few memory latencies, not S.
 __global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a, int64_t rows) {
   const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 16;
   const int r = threadIdx.x % 16;
@@ -286,17 +289,45 @@ __global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a, int64_t r
   const int g = (int)(row - vh * G);
   const int S = a.splits;
   const float* stats = a.stats + vh * S * 2 * G;
+  float m[kMaxSplits], l[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) {
+    m[s] = kNegInf;
+    l[s] = 0.0f;
+    if (s < S) {
+      m[s] = stats[s * 2 * G + g];
+      l[s] = stats[s * 2 * G + G + g];
+    }
+  }
   float M = kNegInf;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, stats[s * 2 * G + g]);
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) M = fmaxf(M, m[s]);
   if (M == kNegInf) M = 0.0f;
   float total = 0.0f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int s = 0; s < S; ++s) {
-    const float l = stats[s * 2 * G + G + g];
-    const float w = l > 0.0f ? exp2_hw(stats[s * 2 * G + g] - M) : 0.0f;
-    total += l * w;
-    const float* p = a.partials + ((vh * S + s) * G + g) * kD + 8 * r;
+  const float* base = a.partials + (vh * S * G + g) * kD + 8 * r;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] += p[j] * w;
+  for (int s0 = 0; s0 < kMaxSplits; s0 += 8) {
+    if (s0 >= S) break;
+    float4 lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      lo[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      hi[i] = lo[i];
+      if (s0 + i < S) {
+        const float4* p = reinterpret_cast<const float4*>(base + (int64_t)(s0 + i) * G * kD);
+        lo[i] = p[0];
+        hi[i] = p[1];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (s0 + i < S) {
+        const float w = l[s0 + i] > 0.0f ? exp2_hw(m[s0 + i] - M) : 0.0f;
+        total += l[s0 + i] * w;
+        acc[0] += lo[i].x * w; acc[1] += lo[i].y * w; acc[2] += lo[i].z * w; acc[3] += lo[i].w * w;
+        acc[4] += hi[i].x * w; acc[5] += hi[i].y * w; acc[6] += hi[i].z * w; acc[7] += hi[i].w * w;
+      }
+    }
   }
   const float den = total > 0.0f ? total : 1.0f;
 #pragma unroll
@@ -306,14 +337,14 @@ __global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a, int64_t r
 
 template <int GT>
 int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
-  // Two sets of U = 2 key blocks in flight (measured best of U = 2, 4, 8 with
-  // and without the second set).  Groups wider than GT (9..16 rows) take two
-  // launches of 8 rows each.
-  constexpr int U = 2;
+  // Two sets of U key blocks in flight (U = 4 measured best for up to 4 query
+  // rows; 2 beyond, within the register budget).  Groups wider than GT
+  // (9..16 rows) take two launches of 8 rows each.
+  constexpr int U = GT <= 4 ? 4 : 2;
   AttnArgs a = args;
   int st = QF_OK;
   for (a.g0 = 0; a.g0 < a.groups && st == QF_OK; a.g0 += GT) {
-    hipLaunchKernelGGL((attn_kernel<GT, U>), dim3((unsigned)vheads, (unsigned)a.splits),
+    hipLaunchKernelGGL((attn_kernel<GT, U, 4>), dim3((unsigned)vheads, (unsigned)a.splits),
                        dim3(kBlock), 0, s, a);
     st = launch_status();
   }
@@ -353,7 +384,7 @@ extern "C" int qf_decode_attention(const void* q, const void* k, const void* v,
   if (batch < 1 || q_heads < 1 || kv_heads < 1 || capacity < 1) return QF_E_ARG;
   if (q_heads % kv_heads != 0 || q_heads / kv_heads > kMaxGroups) return QF_E_SHAPE;
   if (!q || !k || !v || !used || !out) return QF_E_ARG;
-  if (splits < 1 || splits > kMaxSplits || span < 1 || span % kKeysPerIter != 0 ||
+  if (splits < 1 || splits > kMaxSplits || span < 1 || span % kSpanAlign != 0 ||
       (int64_t)splits * span < capacity || (int64_t)(splits - 1) * span >= capacity)
     return QF_E_ARG;
   if (splits > 1 && (!partials || !stats)) return QF_E_ARG;
