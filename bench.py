@@ -349,7 +349,7 @@ def decode_attention_bench(device, replays: int = 20, calls: int = 24) -> dict:
 ENGINE_WORKLOADS = ((1, 512, 32), (4, 2048, 32), (16, 512, 128))
 
 
-def engine_decode(device, steps: int = 32) -> dict:
+def engine_decode(device, steps: int = 32, workloads=ENGINE_WORKLOADS) -> dict:
     """End to end: starter_amd.engine.Engine on a randomly initialised
     Qwen3-4B (the real architecture: 36 layers, hidden 2560, vocab 151936,
     tied embedding) generating at the public workloads; the decode steps are
@@ -368,7 +368,7 @@ def engine_decode(device, steps: int = 32) -> dict:
     weight_bytes += 2 * engine.lm_head.numel()
     out = {"model": "Qwen3-4B architecture, random bf16 weights", "weight_bytes": weight_bytes}
     g = torch.Generator().manual_seed(5)
-    for batch, length, new in ENGINE_WORKLOADS:
+    for batch, length, new in workloads:
         prompts = torch.randint(0, V, (batch, length), generator=g).tolist()
         count = min(new, steps + 1)
         gen = engine.generate(prompts, count)
@@ -537,6 +537,8 @@ def main() -> int:
                     help="skip the decode projections and decode attention")
     ap.add_argument("--no-engine", action="store_true",
                     help="skip the end-to-end Qwen3-4B decode through starter_amd.engine")
+    ap.add_argument("--engine-workload", metavar="B,T,N",
+                    help="run only this engine workload (batch, prompt tokens, new tokens)")
     ap.add_argument("--profile", type=int, default=0, metavar="N",
                     help="only run a calibration copy and N eager launches per prefill kernel "
                          "(for rocprofv3 --pmc), then exit")
@@ -591,7 +593,10 @@ def main() -> int:
                   flush=True)
         projections = {} if args.no_proj else decode_projections(device)
         attention = {} if args.no_proj else decode_attention_bench(device)
-    engine = {} if args.no_engine else engine_decode(device)
+    workloads = ENGINE_WORKLOADS
+    if args.engine_workload:
+        workloads = (tuple(int(v) for v in args.engine_workload.split(",")),)
+    engine = {} if args.no_engine else engine_decode(device, workloads=workloads)
 
     dominant = max(KERNELS, key=lambda n: kernels[n]["us_per_call_mean"])
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": kernels[dominant]["gbps"],
