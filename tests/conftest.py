@@ -4,7 +4,8 @@
 * builds the HIP library / CPU oracle when nothing is built yet;
 * converts between torch bf16 tensors and the oracle's uint16 bit arrays;
 * ``assert_bf16_close``: the parity bar for bf16 outputs - at most ``max_ulp``
-  bf16 ulps from the oracle and within atol/rtol 1e-2.
+  bf16 ulps from the oracle and within atol/rtol 1e-2 (the bf16 tolerance the
+  benchmark definition in BASELINE.json states).
 """
 
 from __future__ import annotations
@@ -55,8 +56,8 @@ def gen(seed: int = 0) -> torch.Generator:
 
 
 def normal(shape, mean=0.0, std=1.0, g=None) -> torch.Tensor:
-    """f32 draws N(mean, std) on a CPU generator, rounded to bf16 (the
-    BASELINE input recipe)."""
+    """f32 draws N(mean, std) on a CPU generator, rounded to bf16 (the input
+    recipe of the BASELINE.json configurations)."""
     return (torch.randn(shape, generator=g, dtype=torch.float32) * std + mean).to(torch.bfloat16)
 
 

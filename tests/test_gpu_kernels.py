@@ -1,7 +1,7 @@
 """GPU parity of every HIP kernel against the CPU oracle (MI355X only).
 
 The bar: the embedding gather, every copied row (V cache) and the bf16
-residual sum are bit-exact, as the BASELINE north star requires.  The norm
+residual sum are bit-exact (integer / byte work has one right answer).  The norm
 and RoPE outputs are bit-exact too: kernel and oracle both sum the exact f32
 squares in f64 and round once, and every later step is a correctly rounded
 f32 operation followed by the same bf16 rounding.  SiLU*up is bit-exact as
@@ -9,8 +9,8 @@ well, proven exhaustively over all 65,536 bf16 gate values (the kernel's fast
 exp2/reciprocal path falls back to the exact f32 formula near bf16 rounding
 midpoints).  The rotary tables (f32 cos / sin of different libraries) must be
 within one bf16 ulp of the oracle with >= 99.9% bit-identical.  Against torch's own GPU
-formulas (a different f32 summation order) the gate is BASELINE's atol/rtol
-1e-2.  Cases follow the reference tests
+formulas (a different f32 summation order) the gate is atol/rtol 1e-2 (the
+benchmark's stated bf16 tolerance).  Cases follow the reference tests
 (tests/test_rmsnorm.py, tests/test_qk_norm_rope.py, tests/test_decode_step.py,
 tests/test_prefill.py) plus the five BASELINE.json configurations at full
 size, ragged/odd shapes that take the scalar paths, empty inputs, NaN-poisoned
