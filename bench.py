@@ -14,8 +14,10 @@ kernel cycles through enough buffer sets that its distinct footprint exceeds
 twice the 256 MB Infinity Cache, so repeated calls cannot be served from it.
 The step is replayed from captured HIP graphs (as the engine replays its
 captured prefill), so host launch overhead is not part of the GPU timeline.
-Per-kernel durations come from HIP events around graphs of 24 back-to-back
-launches of one kernel (rotating its buffer sets), divided by 24.  Decode
+Per-kernel durations come from HIP events around graphs of GRAPH_CALLS (96)
+back-to-back launches of one kernel (rotating its buffer sets), divided by
+96: long enough that the graph's own launch cost adds under 0.1 us per call,
+so the figure matches the kernel trace's average duration.  Decode
 configs 1-3 are timed the same way (microseconds per call), and so are the
 split-K decode projections of one Qwen3-4B layer at batch 1-64, beside the
 F.linear (hipBLASLt) path they replace, and decode attention at the engine
@@ -131,6 +133,7 @@ class Workload:
 
 
 KERNELS = ("embedding", "add_rms_norm", "prefill_qkv", "silu_mul")
+GRAPH_CALLS = 96  # launches per timing graph
 STEPS_PER_GRAPH = 8  # one captured graph holds this many consecutive steps
 
 
@@ -262,7 +265,7 @@ PROJECTIONS = {"qkv": (6144, 2560), "o_proj": (H, 4096), "gate_up": (I, H), "dow
 PROJECTION_ROWS = (1, 4, 16, 64)
 
 
-def decode_projections(device, replays: int = 20, calls: int = 24) -> dict:
+def decode_projections(device, replays: int = 20, calls: int = GRAPH_CALLS) -> dict:
     """Split-K projections (linear_partials / linear_silu_mul) at decode batch
     1-64 on the Qwen3-4B layer shapes, next to the unfused path the engine
     takes without them (F.linear on hipBLASLt, plus silu_mul for gate/up).
@@ -309,7 +312,7 @@ def decode_projections(device, replays: int = 20, calls: int = 24) -> dict:
 ATTENTION_CASES = ((1, 545), (4, 2081), (16, 641))
 
 
-def decode_attention_bench(device, replays: int = 20, calls: int = 24) -> dict:
+def decode_attention_bench(device, replays: int = 20, calls: int = GRAPH_CALLS) -> dict:
     """SmallQueryAttention.run at full cache length on the Qwen3-4B head
     layout (32 query heads, 8 KV heads, width 128), K/V rotating over copies
     beyond twice the Infinity Cache; beside torch's scaled_dot_product_attention
@@ -565,7 +568,7 @@ def main() -> int:
         work = Workload(device)
         torch.cuda.synchronize()
         print(f"bench: buffer sets {work.sets}", file=sys.stderr, flush=True)
-        durations = kernel_durations(work, calls=24, replays=max(10, args.steps // 10))
+        durations = kernel_durations(work, calls=GRAPH_CALLS, replays=max(10, args.steps // 10))
         wall, gpu_seconds = run_prefill_step(work, args.steps, args.warmup)
         ms_per_step = wall * 1e3 / args.steps
         step_bytes = sum(BYTES.values())

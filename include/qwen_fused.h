@@ -233,6 +233,29 @@ int qf_decode_attention(const void* q, const void* k, const void* v, const int32
                         float* stats, void* out, void* stream);
 
 /*
+ * qf_qkv_norm_rope_cache followed by qf_decode_attention on its Q, in the
+ * attention launches (Q never goes to memory):
+ *   qkv (bf16 [batch, (q_heads + 2 kv_heads) * 128], qkv_splits == 0, or f32
+ *   partials [qkv_splits, batch, ...]), q/k gains, eps, cos/sin [capacity, 128]
+ *   and the int64 device position as qf_qkv_norm_rope_cache takes them; the
+ *   caches are the attention's k and v and get the new K/V row at slot
+ *   position (a position outside [0, capacity) writes nothing and gives NaN
+ *   queries, as there); used, scale, (splits, span), scratch and out as
+ *   qf_decode_attention.  Bit-identical to the two calls in sequence.
+ * Replaces the pair engine/decode_step.py:43-47 issues back to back:
+ * qkv_norm_rope_cache (engine/kernels/decode_fused.py:59-118, 172-210) then
+ * SmallQueryAttention.run (engine/kernels/small_query_attention.py:135-158),
+ * saving the Q round trip and one launch per layer.
+ */
+int qf_decode_attention_qkv(const void* qkv, int32_t qkv_splits, const void* q_weight,
+                            const void* k_weight, float q_eps, float k_eps, const void* cos,
+                            const void* sin, const int64_t* position, void* key_cache,
+                            void* value_cache, const int32_t* used, int64_t batch,
+                            int32_t q_heads, int32_t kv_heads, int64_t capacity, float scale,
+                            int32_t splits, int64_t span, float* partials, float* stats,
+                            void* out, void* stream);
+
+/*
  * Candidate slots per row that qf_lm_head_argmax needs (vocab / 16), or a
  * negative status when vocab is not a positive multiple of 16.
  */

@@ -24,6 +24,7 @@
 // the segment, each with its own running state, and are merged in lane-group
 // then wave order at the end.
 #include "qf_device.h"
+#include "qf_rope.h"
 
 namespace qf {
 namespace {
@@ -51,6 +52,21 @@ struct AttnArgs {
   int32_t splits;
   int32_t span;          // keys per segment
   float scale_log2;      // scale * log2(e)
+  // Fused Q/K/V prologue (qf_decode_attention_qkv only): Q comes from the
+  // packed projection row instead of `q`, and the new K/V row goes to slot
+  // *position of the caches (`k` / `v` viewed writable).
+  const void* qkv;       // bf16 [batch, W] or f32 partials [qkv_splits, batch, W]
+  int32_t qkv_splits;    // 0: bf16 rows
+  int32_t kv_heads;
+  int64_t qkv_stride;    // batch * W: f32 elements between partials
+  const uint16_t* qw;
+  const uint16_t* kw;
+  float q_eps, k_eps;
+  const uint16_t* cos;   // [capacity, 128]
+  const uint16_t* sin;
+  const int64_t* position;
+  uint16_t* kc;
+  uint16_t* vc;
 };
 
 __device__ __forceinline__ float dpp_f32_sum16(float x) {
@@ -111,12 +127,23 @@ __device__ __forceinline__ void merge_lanes(State<GT>& s, int mask) {
 // blocks (4 keys per wave each) in flight.  With one segment the workgroup
 // writes the output; otherwise it writes its f32 partials and statistics for
 // attn_merge_kernel.
-template <int GT, int U, int W>
+//
+// FUSED: the workgroup first does qf_qkv_norm_rope_cache's work for its
+// virtual head: lane groups 0..rows-1 fold (or load) and normalise + rotate
+// its query rows, lane groups 8 and 9 its new key and value row, all while the
+// first key blocks are in flight.  Queries reach the other lane groups
+// through LDS.  The segment that owns slot `position` writes the new K/V
+// there (first launch of a wide group only) and uses the new rows in place
+// of whatever the slot held when its loads were issued, so no workgroup
+// reads back its own store.
+template <int GT, int U, int W, bool FUSED>
 __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
   constexpr int kWavesA = W;
   constexpr int kKeysPerIter = kKeysPerWave * W;  // keys per workgroup step
+  static_assert(!FUSED || (W == 4 && GT <= 8), "fused prologue: 16 lane groups, <= 8 query rows");
   __shared__ float xm[kWavesA - 1][GT], xl[kWavesA - 1][GT];
   __shared__ float xacc[kWavesA - 1][GT][kD];
+  __shared__ uint4 qs[FUSED ? GT : 1][16], kvs[2][16];
   const int vh = blockIdx.x;
   const int seg = blockIdx.y;
   const int lane = threadIdx.x % kWave;
@@ -127,12 +154,20 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
   const int rows = G - a.g0 < GT ? G - a.g0 : GT;  // query rows of this launch
 
   uint4 qv[GT];
+  if constexpr (!FUSED) {
 #pragma unroll
-  for (int g = 0; g < GT; ++g)
-    qv[g] = g < rows ? load16<false>(a.q + ((int64_t)vh * G + a.g0 + g) * kD + 8 * r)
-                     : make_uint4(0, 0, 0, 0);
+    for (int g = 0; g < GT; ++g)
+      qv[g] = g < rows ? load16<false>(a.q + ((int64_t)vh * G + a.g0 + g) * kD + 8 * r)
+                       : make_uint4(0, 0, 0, 0);
+  }
 
-  int64_t used = a.used[vh];
+  const int32_t used_in = a.used[vh];
+  // Fused: the new key's slot, read alongside `used` so that the rotary-row
+  // loads it addresses issue as early as the first key blocks (the empty asm
+  // pins both scalar loads here instead of next to their first uses).
+  const int64_t pos_in = FUSED ? *a.position : 0;
+  if constexpr (FUSED) asm volatile("" ::"s"(used_in), "s"(pos_in));
+  int64_t used = used_in;
   used = used < 0 ? 0 : (used > a.capacity ? a.capacity : used);
   const int64_t start = (int64_t)seg * a.span;
   int64_t end = start + a.span;
@@ -155,6 +190,11 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
   const int n = base0 < end ? (int)((end - base0 + step - 1) / step) : 0;
   const int64_t last_key = end - 1;  // a valid slot whenever n > 0
   uint4 kv[2][U], vv[2][U];
+  // Fused: subst marks the segment that attends slot pos, whose new K/V row
+  // (this lane's slice) is knew / vnew.
+  int64_t pos = 0;
+  bool subst = false;
+  uint4 knew = make_uint4(0, 0, 0, 0), vnew = knew;
   // Loads are issued unconditionally (keys past the segment re-read its last
   // valid key, an L2 hit, and are masked out), so the compiler's wait counts
   // stay exact and the next set's loads overlap this set's arithmetic.
@@ -168,6 +208,18 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
     }
   };
   auto consume = [&](int d, int i) {
+    if constexpr (FUSED) {
+      if (subst) {  // the new K/V row replaces slot pos wherever it was loaded
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t key = base0 + i * step + q4 + (int64_t)kKeysPerIter * u;
+          if ((key < end ? key : last_key) == pos) {
+            kv[d][u] = knew;
+            vv[d][u] = vnew;
+          }
+        }
+      }
+    }
     float s[U][GT];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -204,8 +256,56 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
       st.m[g] = mn;
     }
   };
+  if (n > 0) issue(0, 0);
+
+  // Fused prologue (see above).
+  if constexpr (FUSED) {
+    const int lg = wave * 4 + q4;  // lane group 0..15, one DPP row each
+    const int64_t hkv = a.kv_heads;
+    const int64_t b = vh / hkv, h = vh - b * hkv;
+    const int64_t hq = hkv * G;
+    const int64_t width = (hq + 2 * hkv) * kD;
+    pos = pos_in;
+    const bool pos_ok = pos >= 0 && pos < a.capacity;
+    const int64_t slot = pos_ok ? pos : 0;
+    const bool is_q = lg < rows, is_k = lg == 8, is_v = lg == 9;
+    const bool live = is_q || is_k || is_v;
+    const int64_t head = is_q ? h * G + a.g0 + lg : is_k ? hq + h : hq + hkv + h;
+    const int64_t off = b * width + head * kD + 8 * r;
+    // Gains and rotary rows first: the fold below waits for its loads, and
+    // these should already be in flight by then.
+    const uint4 wv = load16<false>((is_q ? a.qw : a.kw) + 8 * r);
+    const uint4 cv = load16<false>(a.cos + slot * kD + 8 * r);
+    const uint4 sv = load16<false>(a.sin + slot * kD + 8 * r);
+    float x[8];
+    uint4 xv;
+    if (a.qkv_splits == 0) {
+      xv = live ? load16<false>(static_cast<const uint16_t*>(a.qkv) + off) : make_uint4(0, 0, 0, 0);
+    } else {
+      sum_partials8<8>(static_cast<const float*>(a.qkv) + off, a.qkv_stride, a.qkv_splits, live, x);
+      xv = pack8(x);  // one rounding of the f32 sum
+    }
+    unpack8(xv, x);
+    const uint4 o = norm_rope(x, wv, cv, sv, is_q ? a.q_eps : a.k_eps, r);  // every lane: DPP
+    const uint4 nan4 = make_uint4(0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u);
+    if (is_q) qs[lg][r] = select4(pos_ok, o, nan4);
+    if (is_k) kvs[0][r] = o;
+    if (is_v) kvs[1][r] = xv;
+    const bool owns_slot = pos_ok && pos >= start && pos < start + a.span;
+    if (owns_slot && a.g0 == 0 && (is_k || is_v))
+      store16<false>((is_k ? a.kc : a.vc) + ((int64_t)vh * a.capacity + pos) * kD + 8 * r,
+                     select4(is_k, o, xv));
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < GT; ++g) qv[g] = g < rows ? qs[g][r] : make_uint4(0, 0, 0, 0);
+    subst = owns_slot && pos < end;
+    if (subst) {
+      knew = kvs[0][r];
+      vnew = kvs[1][r];
+    }
+  }
+
   if (n > 0) {
-    issue(0, 0);
     for (int i = 0;; i += 2) {
       issue(1, i + 1);
       consume(0, i);
@@ -278,8 +378,9 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
 
 // One 16-lane group per query row (4 rows per wave): weights 2^(m_s - M)
 // for segments with a positive denominator, summed in segment order.  All
-// statistics, then the partials in groups of 8 segments, are loaded before
-// they are combined, so the kernel waits a few memory latencies, not S.
+// statistics, then the partials in groups of 16 segments, are loaded before
+// they are combined, so the kernel waits one or two memory latencies, not S.
+constexpr int kMergeBatch = 16;
 __global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a, int64_t rows) {
   const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 16;
   const int r = threadIdx.x % 16;
@@ -306,11 +407,11 @@ __global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a, int64_t r
   float total = 0.0f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const float* base = a.partials + (vh * S * G + g) * kD + 8 * r;
 #pragma unroll
-  for (int s0 = 0; s0 < kMaxSplits; s0 += 8) {
+  for (int s0 = 0; s0 < kMaxSplits; s0 += kMergeBatch) {
     if (s0 >= S) break;
-    float4 lo[8], hi[8];
+    float4 lo[kMergeBatch], hi[kMergeBatch];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kMergeBatch; ++i) {
       lo[i] = make_float4(0.f, 0.f, 0.f, 0.f);
       hi[i] = lo[i];
       if (s0 + i < S) {
@@ -320,7 +421,7 @@ __global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a, int64_t r
       }
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kMergeBatch; ++i) {
       if (s0 + i < S) {
         const float w = l[s0 + i] > 0.0f ? exp2_hw(m[s0 + i] - M) : 0.0f;
         total += l[s0 + i] * w;
@@ -335,7 +436,7 @@ __global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a, int64_t r
   store16<false>(a.out + row * kD + 8 * r, pack8(acc));
 }
 
-template <int GT>
+template <int GT, bool FUSED>
 int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
   // Two sets of U key blocks in flight (U = 4 measured best for up to 4 query
   // rows; 2 beyond, within the register budget).  Groups wider than GT
@@ -344,7 +445,7 @@ int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
   AttnArgs a = args;
   int st = QF_OK;
   for (a.g0 = 0; a.g0 < a.groups && st == QF_OK; a.g0 += GT) {
-    hipLaunchKernelGGL((attn_kernel<GT, U, 4>), dim3((unsigned)vheads, (unsigned)a.splits),
+    hipLaunchKernelGGL((attn_kernel<GT, U, 4, FUSED>), dim3((unsigned)vheads, (unsigned)a.splits),
                        dim3(kBlock), 0, s, a);
     st = launch_status();
   }
@@ -376,24 +477,26 @@ extern "C" int qf_attention_partition(int64_t virtual_heads, int64_t capacity,
   return QF_OK;
 }
 
-extern "C" int qf_decode_attention(const void* q, const void* k, const void* v,
-                                   const int32_t* used, int64_t batch, int32_t q_heads,
-                                   int32_t kv_heads, int64_t capacity, float scale,
-                                   int32_t splits, int64_t span, float* partials, float* stats,
-                                   void* out, void* stream) {
+namespace {
+
+// Checks shared by both entry points (query source `qsrc`: q, or the packed
+// projection row of the fused entry) and the attention half of the arguments.
+int attention_setup(const void* qsrc, const void* k, const void* v, const int32_t* used,
+                    int64_t batch, int32_t q_heads, int32_t kv_heads, int64_t capacity,
+                    float scale, int32_t splits, int64_t span, float* partials, float* stats,
+                    void* out, AttnArgs& a, int64_t& vheads) {
   if (batch < 1 || q_heads < 1 || kv_heads < 1 || capacity < 1) return QF_E_ARG;
   if (q_heads % kv_heads != 0 || q_heads / kv_heads > kMaxGroups) return QF_E_SHAPE;
-  if (!q || !k || !v || !used || !out) return QF_E_ARG;
+  if (!qsrc || !k || !v || !used || !out) return QF_E_ARG;
   if (splits < 1 || splits > kMaxSplits || span < 1 || span % kSpanAlign != 0 ||
       (int64_t)splits * span < capacity || (int64_t)(splits - 1) * span >= capacity)
     return QF_E_ARG;
   if (splits > 1 && (!partials || !stats)) return QF_E_ARG;
   if (!(scale == scale) || scale == __builtin_inff() || scale == kNegInf) return QF_E_ARG;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return QF_E_ALIGN;
-  const int64_t vheads = batch * kv_heads;
+  if (!aligned16(qsrc) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return QF_E_ALIGN;
+  vheads = batch * kv_heads;
   if (vheads > INT32_MAX) return QF_E_SHAPE;
-  AttnArgs a;
-  a.q = static_cast<const uint16_t*>(q);
+  a = AttnArgs{};
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
   a.used = used;
@@ -406,11 +509,63 @@ extern "C" int qf_decode_attention(const void* q, const void* k, const void* v,
   a.splits = splits;
   a.span = (int32_t)span;
   a.scale_log2 = (float)((double)scale * 1.4426950408889634);
-  hipStream_t s = as_stream(stream);
+  a.kv_heads = kv_heads;
+  return QF_OK;
+}
+
+template <bool FUSED>
+int dispatch_attn(const AttnArgs& a, int64_t vheads, hipStream_t s) {
   switch (a.groups) {
-    case 1: return launch_attn<1>(a, vheads, s);
-    case 2: return launch_attn<2>(a, vheads, s);
-    case 3: case 4: return launch_attn<4>(a, vheads, s);
-    default: return launch_attn<8>(a, vheads, s);
+    case 1: return launch_attn<1, FUSED>(a, vheads, s);
+    case 2: return launch_attn<2, FUSED>(a, vheads, s);
+    case 3: case 4: return launch_attn<4, FUSED>(a, vheads, s);
+    default: return launch_attn<8, FUSED>(a, vheads, s);
   }
+}
+
+}  // namespace
+
+extern "C" int qf_decode_attention(const void* q, const void* k, const void* v,
+                                   const int32_t* used, int64_t batch, int32_t q_heads,
+                                   int32_t kv_heads, int64_t capacity, float scale,
+                                   int32_t splits, int64_t span, float* partials, float* stats,
+                                   void* out, void* stream) {
+  AttnArgs a;
+  int64_t vheads = 0;
+  const int st = attention_setup(q, k, v, used, batch, q_heads, kv_heads, capacity, scale, splits,
+                                 span, partials, stats, out, a, vheads);
+  if (st != QF_OK) return st;
+  a.q = static_cast<const uint16_t*>(q);
+  return dispatch_attn<false>(a, vheads, as_stream(stream));
+}
+
+extern "C" int qf_decode_attention_qkv(const void* qkv, int32_t qkv_splits, const void* q_weight,
+                                       const void* k_weight, float q_eps, float k_eps,
+                                       const void* cos, const void* sin, const int64_t* position,
+                                       void* key_cache, void* value_cache, const int32_t* used,
+                                       int64_t batch, int32_t q_heads, int32_t kv_heads,
+                                       int64_t capacity, float scale, int32_t splits, int64_t span,
+                                       float* partials, float* stats, void* out, void* stream) {
+  AttnArgs a;
+  int64_t vheads = 0;
+  const int st = attention_setup(qkv, key_cache, value_cache, used, batch, q_heads, kv_heads,
+                                 capacity, scale, splits, span, partials, stats, out, a, vheads);
+  if (st != QF_OK) return st;
+  if (qkv_splits < 0 || !q_weight || !k_weight || !cos || !sin || !position) return QF_E_ARG;
+  if (!aligned16(q_weight) || !aligned16(k_weight) || !aligned16(cos) || !aligned16(sin) ||
+      (reinterpret_cast<uintptr_t>(position) & 7u))
+    return QF_E_ALIGN;
+  a.qkv = qkv;
+  a.qkv_splits = qkv_splits;
+  a.qkv_stride = batch * ((int64_t)q_heads + 2 * (int64_t)kv_heads) * kD;
+  a.qw = static_cast<const uint16_t*>(q_weight);
+  a.kw = static_cast<const uint16_t*>(k_weight);
+  a.q_eps = q_eps;
+  a.k_eps = k_eps;
+  a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin);
+  a.position = position;
+  a.kc = static_cast<uint16_t*>(key_cache);
+  a.vc = static_cast<uint16_t*>(value_cache);
+  return dispatch_attn<true>(a, vheads, as_stream(stream));
 }

@@ -11,8 +11,9 @@ reference runs:
   projection (hipBLASLt), ``prefill_qkv`` (Q/K norm + RoPE + K/V cache write),
   causal attention, and the residual-add + RMSNorm / SiLU * up fusions;
 * decode (``engine/decode_step.py:33-64``): the split-K projections whose f32
-  partials feed ``qkv_norm_rope_cache`` and ``add_rms_norm``, the fused
-  gate/up projection with its SiLU epilogue, split-KV decode attention, and
+  partials feed ``add_rms_norm`` and the split-KV decode attention (which
+  also does ``qkv_norm_rope_cache``'s Q/K norm, RoPE and cache write in its
+  own launches), the fused gate/up projection with its SiLU epilogue, and
   the LM head fused with the greedy token choice; the whole step is captured once per
   (batch, capacity) in a HIP graph and replayed with the position and cache
   lengths advanced on the device.
@@ -31,7 +32,7 @@ from dataclasses import dataclass
 import torch
 from torch.nn import functional as F
 
-from .kernels.decode_fused import add_rms_norm, qkv_norm_rope_cache, silu_mul
+from .kernels.decode_fused import add_rms_norm, silu_mul
 from .kernels.embedding import embedding
 from .kernels import lm_head as _lm_head
 from .kernels.prefill import prefill_qkv
@@ -209,10 +210,11 @@ class Engine:
         first = self.layers[0]
         normed = rms_norm(x, first.ln_in, first.eps_in)
         for index, layer in enumerate(self.layers):
-            q = qkv_norm_rope_cache(self._project(normed, layer.qkv), layer.q_norm, layer.k_norm,
-                                    layer.eps_q, layer.eps_k, st.cos, st.sin, st.position,
-                                    st.keys[index], st.values[index])
-            attended = st.attention.run(q, st.keys[index], st.values[index], st.used, self.scale)
+            # qkv_norm_rope_cache + attention, fused into the attention launches
+            attended = st.attention.run_qkv(self._project(normed, layer.qkv), layer.q_norm,
+                                            layer.k_norm, layer.eps_q, layer.eps_k, st.cos, st.sin,
+                                            st.position, st.keys[index], st.values[index],
+                                            st.used, self.scale)
             x, normed = add_rms_norm(x, self._project(attended.view(batch, -1), layer.o),
                                      layer.ln_post, layer.eps_post)
             hidden = self._mlp_hidden(normed, layer.gate_up)

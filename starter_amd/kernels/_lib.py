@@ -45,6 +45,9 @@ SIGNATURES = {
     "qf_attention_partition": ([_i64, _i64, _i32, _vp, _vp], _i32),
     "qf_decode_attention": ([_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _f32, _i32, _i64, _vp, _vp,
                              _vp, _vp], _i32),
+    "qf_decode_attention_qkv": ([_vp, _i32, _vp, _vp, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                 _i64, _i32, _i32, _i64, _f32, _i32, _i64, _vp, _vp, _vp, _vp],
+                                _i32),
     "qf_lm_head_blocks": ([_i64], _i64),
     "qf_lm_head_argmax": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp], _i32),
 }

@@ -84,3 +84,42 @@ class SmallQueryAttention:
                   self.splits, self.span, self.partials.data_ptr(), self.stats.data_ptr(),
                   out.data_ptr(), _lib.stream(device))
         return out
+
+    def run_qkv(self, qkv, q_weight, k_weight, q_eps, k_eps, cos, sin, position,
+                key_cache, value_cache, used, scale):
+        """``qkv_norm_rope_cache`` followed by ``run`` on its Q, in the attention
+        launches: the call pair engine/decode_step.py:43-47 makes, with the
+        same arguments and the same results bit for bit (the new K/V row lands
+        in slot ``position`` of the caches, Q never goes to memory).  ``qkv``
+        is BF16 [B, (Hq + 2 Hkv) * 128] or FP32 split-K partials [S, B, ...]."""
+        device = self.partials.device
+        width = (self.hq + 2 * self.hk) * HEAD
+        if qkv.dtype == torch.float32 and qkv.ndim == 3:
+            qkv_splits = qkv.shape[0]
+            ok = qkv_splits >= 1 and tuple(qkv.shape[1:]) == (self.batch, width)
+        else:
+            qkv_splits = 0
+            ok = qkv.dtype == torch.bfloat16 and tuple(qkv.shape) == (self.batch, width)
+        bf16 = (q_weight, k_weight, cos, sin, key_cache, value_cache)
+        if (torch.is_grad_enabled() or not ok or not qkv.is_contiguous() or qkv.device != device
+                or not math.isfinite(scale)
+                or tuple(q_weight.shape) != (HEAD,) or tuple(k_weight.shape) != (HEAD,)
+                or tuple(cos.shape) != (self.capacity, HEAD) or sin.shape != cos.shape
+                or tuple(position.shape) != (1,) or position.dtype != torch.int64
+                or position.device != device
+                or key_cache.shape != (self.batch, self.hk, self.capacity, HEAD)
+                or value_cache.shape != key_cache.shape
+                or used.shape != (self.virtual_heads,) or used.dtype != torch.int32
+                or used.device != device or not used.is_contiguous()
+                or any(t.dtype != torch.bfloat16 or t.device != device or not t.is_contiguous()
+                       for t in bf16)):
+            raise ValueError("expected packed BF16 Q/K/V (or FP32 partials), BF16 gains, rotary "
+                             "tables and caches, an int64 position and int32 lengths on one device")
+        out = torch.empty((self.batch, 1, self.hq, HEAD), dtype=torch.bfloat16, device=device)
+        _lib.call("qf_decode_attention_qkv", qkv.data_ptr(), qkv_splits, q_weight.data_ptr(),
+                  k_weight.data_ptr(), float(q_eps), float(k_eps), cos.data_ptr(), sin.data_ptr(),
+                  position.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+                  used.data_ptr(), self.batch, self.hq, self.hk, self.capacity, float(scale),
+                  self.splits, self.span, self.partials.data_ptr(), self.stats.data_ptr(),
+                  out.data_ptr(), _lib.stream(device))
+        return out

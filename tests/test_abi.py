@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 17
+    assert len(names) == 18
 
 
 def test_library_exports_every_symbol():
@@ -102,6 +102,20 @@ def test_host_side_argument_errors_launch_nothing():
                                    None, None, bogus, None) == -1
     assert lib.qf_decode_attention(bogus + 2, bogus, bogus, bogus, 1, 8, 2, 64, 0.1, 1, 64, None,
                                    None, bogus, None) == -3
+    # fused Q/K/V + attention: the attention rules, then the Q/K/V operands
+    fused = lib.qf_decode_attention_qkv
+    assert fused(bogus, 0, bogus, bogus, 1e-6, 1e-6, bogus, bogus, bogus, bogus, bogus, bogus,
+                 1, 34, 2, 64, 0.1, 1, 64, None, None, bogus, None) == -2
+    assert fused(bogus, 0, bogus, bogus, 1e-6, 1e-6, bogus, bogus, bogus, bogus, bogus, bogus,
+                 1, 8, 2, 545, 0.1, 9, 64, None, None, bogus, None) == -1
+    assert fused(bogus, -1, bogus, bogus, 1e-6, 1e-6, bogus, bogus, bogus, bogus, bogus, bogus,
+                 1, 8, 2, 64, 0.1, 1, 64, None, None, bogus, None) == -1
+    assert fused(bogus, 0, bogus, bogus, 1e-6, 1e-6, bogus, bogus, None, bogus, bogus, bogus,
+                 1, 8, 2, 64, 0.1, 1, 64, None, None, bogus, None) == -1   # no position
+    assert fused(bogus, 0, bogus, bogus, 1e-6, 1e-6, bogus, bogus, bogus + 4, bogus, bogus, bogus,
+                 1, 8, 2, 64, 0.1, 1, 64, None, None, bogus, None) == -3   # misaligned position
+    assert fused(bogus + 2, 0, bogus, bogus, 1e-6, 1e-6, bogus, bogus, bogus, bogus, bogus, bogus,
+                 1, 8, 2, 64, 0.1, 1, 64, None, None, bogus, None) == -3
 
 
 def test_empty_inputs_are_no_ops():

@@ -399,6 +399,27 @@ def test_attention_context_validation_and_marshalling():
             plan.run(*bad_args)
     with pytest.raises(ValueError):  # autograd enabled
         plan.run(q, k, k, used, 0.25)
+    # fused Q/K/V prologue: f32 partials or bf16 rows, gains, tables, device position
+    parts = Fake((8, 2, (8 + 2 * 2) * 128), dtype=torch.float32)
+    gain, table, pos = Fake((128,)), Fake((257, 128)), Fake((1,), dtype=torch.int64)
+    with recorded() as calls, torch.no_grad():
+        out = plan.run_qkv(parts, gain, gain, 1e-6, 2e-6, table, table, pos, k, k, used, 0.25)
+        plan.run_qkv(Fake((2, 12 * 128)), gain, gain, 1e-6, 2e-6, table, table, pos, k, k, used, 0.5)
+    assert tuple(out.shape) == (2, 1, 8, 128)
+    name, *args = calls[0]
+    assert name == "qf_decode_attention_qkv"
+    assert args[1] == 8 and args[4:6] == [1e-6, 2e-6] and args[8] == pos.data_ptr()
+    assert args[12:19] == [2, 8, 2, 257, 0.25, plan.splits, plan.span]
+    assert calls[1][2] == 0  # bf16 rows: no partials
+    good = [parts, gain, gain, 1e-6, 2e-6, table, table, pos, k, k, used, 0.25]
+    for index, bad in ((0, Fake((8, 2, 11 * 128), dtype=torch.float32)),   # wrong packed width
+                       (0, Fake((2, 12 * 128), dtype=torch.float16)),
+                       (5, Fake((256, 128))),                                # table != capacity
+                       (7, Fake((1,), dtype=torch.int32)),
+                       (8, Fake((2, 2, 256, 128))),
+                       (11, float("inf"))):
+        with pytest.raises(ValueError), torch.no_grad():
+            plan.run_qkv(*good[:index], bad, *good[index + 1:])
 
 
 def test_lm_head_rule_and_marshalling():
