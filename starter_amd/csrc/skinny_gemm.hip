@@ -102,6 +102,116 @@ constexpr int kLdsRow = kChunk * 2 + 16;       // padded staging row: 144 bytes
 constexpr int kTileLds = kTile * kLdsRow;      // one 16-row staging tile
 constexpr int kRowsPerLoad = kWave * 16 / (kChunk * 2);  // 8 rows x 128 B per load
 
+// Wave hand-off and epilogue shared by the kernel variants: waves wk > 0 of
+// each n-tile group pass their f32 tiles through LDS to wave wk = 0, which
+// adds them in wave order and writes the partials, the SiLU * up product or
+// the argmax candidates.  Called by every wave of the workgroup.
+template <int MT, int NT, int WK, int EPI>
+__device__ __forceinline__ void finish(const SkinnyArgs& a, f32x4 (&acc)[NT][MT], uint8_t* lds,
+                                       int lane, int wk, int wn, int col0, bool live, int split) {
+  constexpr bool PAIRS = EPI == kEpiSiluMul;
+  constexpr int kCols = PAIRS ? NT / 2 : NT;
+  const int r = lane % kTile;
+  const int g = lane / kTile;
+  // Waves wk = 1..WK-1 of each group hand their tiles to the group's wave
+  // wk = 0, which adds them in wave order.
+  if constexpr (WK > 1) {
+    __syncthreads();
+    f32x4* handoff = reinterpret_cast<f32x4*>(lds);
+    constexpr int kPer = NT * MT * kWave;
+    if (wk > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          handoff[(wn * (WK - 1) + wk - 1) * kPer + (t * MT + mt) * kWave + lane] = acc[t][mt];
+    }
+    __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int w = 0; w < WK - 1; ++w)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[t][mt] += handoff[(wn * (WK - 1) + w) * kPer + (t * MT + mt) * kWave + lane];
+  }
+
+  if constexpr (EPI == kEpiArgmax) {
+    // bf16 logits of this workgroup's 16*NT columns; per row the largest,
+    // lowest column on ties (NaN counts as largest), reduced over the four
+    // lanes that hold a row (all lanes take part in the shuffles).
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = kTile * mt + r;
+      const bool row_ok = live && m < a.m;
+      float best = -__builtin_inff();
+      int besti = INT32_MAX;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = from_bf16(to_bf16(acc[t][mt][i]));
+          const int col = col0 + kTile * t + 4 * g + i;
+          if (better(v[i], col, best, besti)) {
+            best = v[i];
+            besti = col;
+          }
+        }
+        if (row_ok && a.out)
+          *reinterpret_cast<uint2*>(a.out + (int64_t)m * a.n + col0 + kTile * t + 4 * g) =
+              make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+      }
+#pragma unroll
+      for (int mask = 16; mask <= 32; mask *= 2) {
+        const float ov = __shfl_xor(best, mask);
+        const int oi = __shfl_xor(besti, mask);
+        if (better(ov, oi, best, besti)) {
+          best = ov;
+          besti = oi;
+        }
+      }
+      if (row_ok && g == 0) {
+        uint2* cand = reinterpret_cast<uint2*>(a.partials) + (int64_t)m * gridDim.x + blockIdx.x;
+        *cand = make_uint2(__float_as_uint(best), (uint32_t)besti);
+      }
+    }
+    return;
+  }
+  if (!live) return;
+  if constexpr (!PAIRS) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = kTile * mt + r;
+      if (m >= a.m) continue;
+      float* dst = a.partials + ((int64_t)split * a.m + m) * a.n + col0 + 4 * g;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) *reinterpret_cast<f32x4*>(dst + kTile * t) = acc[t][mt];
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = kTile * mt + r;
+      if (m >= a.m) continue;
+      uint16_t* dst = a.out + (int64_t)m * a.n + col0 + 4 * g;
+#pragma unroll
+      for (int h = 0; h < kCols; ++h) {
+        float y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // Each projection is a bf16 tensor in the reference; SiLU is
+          // rounded to bf16 before the bf16 product.
+          const float gate = from_bf16(to_bf16(acc[h][mt][i]));
+          const float up = from_bf16(to_bf16(acc[kCols + h][mt][i]));
+          y[i] = from_bf16(to_bf16(silu_f32(gate))) * up;
+        }
+        *reinterpret_cast<uint2*>(dst + kTile * h) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+      }
+    }
+  }
+}
+
 // MT m-tiles of x (M <= 16*MT); NT n-tiles of W per wave (for PAIRS the
 // first NT/2 are gate tiles, the rest the matching up tiles); the four waves
 // form WN = 4/WK groups of distinct n-tiles, each group WK waves that split
@@ -249,103 +359,160 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
       if (d < n_own) consume(d);
   }
 
-  // Waves wk = 1..WK-1 of each group hand their tiles to the group's wave
-  // wk = 0, which adds them in wave order.
-  if constexpr (WK > 1) {
-    __syncthreads();
-    f32x4* handoff = reinterpret_cast<f32x4*>(lds);
-    constexpr int kPer = NT * MT * kWave;
-    if (wk > 0) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          handoff[(wn * (WK - 1) + wk - 1) * kPer + (t * MT + mt) * kWave + lane] = acc[t][mt];
-    }
-    __syncthreads();
-    if (wk > 0) return;
-#pragma unroll
-    for (int w = 0; w < WK - 1; ++w)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          acc[t][mt] += handoff[(wn * (WK - 1) + w) * kPer + (t * MT + mt) * kWave + lane];
-  }
+  finish<MT, NT, WK, EPI>(a, acc, lds, lane, wk, wn, col0, live, split);
+}
 
-  if constexpr (EPI == kEpiArgmax) {
-    // bf16 logits of this workgroup's 16*NT columns; per row the largest,
-    // lowest column on ties (NaN counts as largest), reduced over the four
-    // lanes that hold a row (all lanes take part in the shuffles).
+// Variant for 17..64 rows of x, where re-reading x dominates: with the
+// waves of a workgroup splitting K, every workgroup reads its whole x slice
+// from L2 for only 16*NT output columns.  Here the WN = 4 / WK wave groups
+// take distinct n-tiles of the same chunks, and the workgroup stages each x
+// chunk once, cooperatively and coalesced, in a shared LDS ring of two
+// buffers (one barrier per step: a buffer is rewritten only after every wave
+// has passed the barrier that follows its last read).  A step covers WK
+// chunks, one per wave of a group; W still goes through each wave's private
+// staging tile.  All waves run the same number of steps (chunks % WK == 0);
+// waves whose n-tiles lie past N stream row 0 and store nothing.
+template <int MT, int NT, int WK, int D, int EPI, bool NTL>
+__global__ __launch_bounds__(kBlock) void skinny_xs_kernel(SkinnyArgs a) {
+  constexpr bool PAIRS = EPI == kEpiSiluMul;
+  static_assert(kWaves % WK == 0, "wave split");
+  constexpr int WN = kWaves / WK;
+  constexpr int kCols = PAIRS ? NT / 2 : NT;
+  constexpr int kRows = kTile * MT;                       // staged x rows (M padded)
+  constexpr int kPieces = WK * kRows * (kChunk * 2 / 16);  // 16-byte pieces per step
+  constexpr int XL = (kPieces + kBlock - 1) / kBlock;      // x loads per thread per step
+  constexpr int kXStep = WK * kRows * kLdsRow;             // one ring buffer
+  constexpr int kWStage = kWaves * NT * kTileLds;
+  constexpr int kStageBytes = 2 * kXStep + kWStage;
+  constexpr int kHandoffBytes = WN * (WK - 1) * NT * MT * kWave * 16;
+  __shared__ __attribute__((aligned(16)))
+      uint8_t lds[kStageBytes > kHandoffBytes ? kStageBytes : kHandoffBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int r = lane % kTile;
+  const int g = lane / kTile;
+  const int wk = wave % WK;
+  const int wn = wave / WK;
+  const int col0 = (blockIdx.x * WN + wn) * (kTile * kCols);
+  const bool live = col0 < a.n;
+  const int split = blockIdx.y;
+  const int64_t kbase = (int64_t)split * a.chunks * kChunk;
+
+  const uint16_t* wp[NT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = kTile * mt + r;
-      const bool row_ok = live && m < a.m;
-      float best = -__builtin_inff();
-      int besti = INT32_MAX;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[i] = from_bf16(to_bf16(acc[t][mt][i]));
-          const int col = col0 + kTile * t + 4 * g + i;
-          if (better(v[i], col, best, besti)) {
-            best = v[i];
-            besti = col;
-          }
-        }
-        if (row_ok && a.out)
-          *reinterpret_cast<uint2*>(a.out + (int64_t)m * a.n + col0 + kTile * t + 4 * g) =
-              make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
-      }
-#pragma unroll
-      for (int mask = 16; mask <= 32; mask *= 2) {
-        const float ov = __shfl_xor(best, mask);
-        const int oi = __shfl_xor(besti, mask);
-        if (better(ov, oi, best, besti)) {
-          best = ov;
-          besti = oi;
-        }
-      }
-      if (row_ok && g == 0) {
-        uint2* cand = reinterpret_cast<uint2*>(a.partials) + (int64_t)m * gridDim.x + blockIdx.x;
-        *cand = make_uint2(__float_as_uint(best), (uint32_t)besti);
-      }
-    }
-    return;
+  for (int t = 0; t < NT; ++t) {
+    int row = col0 + kTile * t;
+    if (PAIRS && t >= kCols) row = a.n + col0 + kTile * (t - kCols);
+    if (!live) row = 0;
+    wp[t] = a.w + (int64_t)(row + lane / 8) * a.k + kbase + 8 * (lane % 8);
   }
-  if (!live) return;
-  if constexpr (!PAIRS) {
+  const int64_t wstep = (int64_t)kRowsPerLoad * a.k;
+
+  // Piece p = tid + 256 i of a step: chunk wk' = p / (8 kRows) of the step,
+  // x row (p / 8) % kRows (row 0 stands in for rows past M), 16 bytes at
+  // column 8 * (p % 8) of the chunk.
+  const uint16_t* xp[XL];
+  int xoff[XL];
+  bool xon[XL];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = kTile * mt + r;
-      if (m >= a.m) continue;
-      float* dst = a.partials + ((int64_t)split * a.m + m) * a.n + col0 + 4 * g;
+  for (int i = 0; i < XL; ++i) {
+    const int p = tid + kBlock * i;
+    xon[i] = p < kPieces;
+    const int pc = xon[i] ? p : 0;
+    const int wkp = pc / (8 * kRows);
+    const int row = (pc / 8) % kRows;
+    xp[i] = a.x + (int64_t)(row < a.m ? row : 0) * a.k + kbase + (int64_t)wkp * kChunk + 8 * (pc % 8);
+    xoff[i] = (wkp * kRows + row) * kLdsRow + 16 * (pc % 8);
+  }
+  uint8_t* xring = lds;
+  uint8_t* stage = lds + 2 * kXStep + wave * NT * kTileLds;
+  const int wr_off = (lane / 8) * kLdsRow + 16 * (lane % 8);
+  const int rd_off = r * kLdsRow + 16 * g;
+  const int xrd_off = wk * kRows * kLdsRow + rd_off;
+
+  f32x4 acc[NT][MT];
 #pragma unroll
-      for (int t = 0; t < NT; ++t) *reinterpret_cast<f32x4*>(dst + kTile * t) = acc[t][mt];
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  uint4 wv[D][NT][2], xv[D][XL];
+  const int steps = a.chunks / WK;  // the same for every wave
+
+  auto issue = [&](int d, int j) {
+    const int64_t off = (int64_t)(wk + WK * j) * kChunk;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) wv[d][t][i] = load16<NTL>(wp[t] + off + i * wstep);
+    const int64_t xstep = (int64_t)WK * j * kChunk;
+#pragma unroll
+    for (int i = 0; i < XL; ++i) xv[d][i] = xon[i] ? load16<false>(xp[i] + xstep) : make_uint4(0, 0, 0, 0);
+  };
+  auto consume = [&](int d, int j) {
+    uint8_t* xb = xring + (j & 1) * kXStep;
+#pragma unroll
+    for (int i = 0; i < XL; ++i)
+      if (xon[i]) *reinterpret_cast<uint4*>(xb + xoff[i]) = xv[d][i];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        *reinterpret_cast<uint4*>(stage + t * kTileLds + wr_off + i * kRowsPerLoad * kLdsRow) =
+            wv[d][t][i];
+    __syncthreads();
+    uint4 fw[NT][2], fx[MT][2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        fw[t][s] = *reinterpret_cast<const uint4*>(stage + t * kTileLds + rd_off + s * kStep * 2);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        fx[mt][s] = *reinterpret_cast<const uint4*>(xb + xrd_off + mt * kTileLds + s * kStep * 2);
     }
+    wave_lds_fence();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma(fw[t][s], fx[mt][s], acc[t][mt]);
+  };
+
+  // The same software pipeline as skinny_kernel, D steps in flight.
+  if (steps >= D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, d);
+    int j = 0;
+    for (; j + 2 * D <= steps; j += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        consume(d, j + d);
+        issue(d, j + d + D);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      consume(d, j + d);
+      if (j + d + D < steps) issue(d, j + d + D);
+    }
+    j += D;
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (j + d < steps) consume(d, j + d);
   } else {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = kTile * mt + r;
-      if (m >= a.m) continue;
-      uint16_t* dst = a.out + (int64_t)m * a.n + col0 + 4 * g;
+    for (int d = 0; d < D; ++d)
+      if (d < steps) issue(d, d);
 #pragma unroll
-      for (int h = 0; h < kCols; ++h) {
-        float y[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          // Each projection is a bf16 tensor in the reference; SiLU is
-          // rounded to bf16 before the bf16 product.
-          const float gate = from_bf16(to_bf16(acc[h][mt][i]));
-          const float up = from_bf16(to_bf16(acc[kCols + h][mt][i]));
-          y[i] = from_bf16(to_bf16(silu_f32(gate))) * up;
-        }
-        *reinterpret_cast<uint2*>(dst + kTile * h) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
-      }
-    }
+    for (int d = 0; d < D; ++d)
+      if (d < steps) consume(d, d);
   }
+
+  finish<MT, NT, WK, EPI>(a, acc, lds, lane, wk, wn, col0, live, split);
 }
 
 // ---- launch plans -----------------------------------------------------------
@@ -357,15 +524,40 @@ int shape_status(int64_t rows, int64_t k, int64_t n) {
   return QF_OK;
 }
 
-// Power-of-two K splits (measured on the Qwen3-4B projection shapes):
-// as many as keep every wave at least one chunk, the grid at most 3072
-// workgroups of 16 columns (~12 per CU), and the partials (written here, read
-// by the consumer) small: splits * min(M, 16) <= K / 32.
+// Shared-x wave layout for 17..64 rows (measured on the Qwen3-4B shapes at
+// M = 32, 48, 64): wide outputs take one n-tile per wave and four waves per
+// chunk step; narrower ones two n-tiles per wave and two chunks per step
+// (one per wave pair) when K is short, else one tile per wave with a deeper
+// pipeline.  D = steps in flight per wave.
+struct XsPlan {
+  int nt, wk, d;
+};
+XsPlan xs_plan(int64_t rows, int64_t k, int64_t n) {
+  if (n >= 4096) return {1, 1, rows <= 32 ? 4 : 6};
+  if (k <= 4096) return {2, 2, 4};
+  return {1, 1, 6};
+}
+
+// Power-of-two K splits (measured on the Qwen3-4B projection shapes).  Up to
+// 16 rows: as many as keep every wave at least one chunk, the grid at most
+// 3072 workgroups of 16 columns (~12 per CU), and the partials (written here,
+// read by the consumer) small: splits * min(M, 16) <= K / 32.  Beyond 16 rows
+// (shared-x kernel): the fewest that give ~150 workgroups, within the same
+// partials bound and whole steps per split.
 int plan_splits(int64_t rows, int64_t k, int64_t n) {
   const int64_t chunks = k / kChunk;
-  const int64_t tiles = n / kTile;
   const int64_t mrows = rows < kTile ? rows : kTile;
   int64_t s = 1;
+  if (rows > kTile) {
+    const XsPlan p = xs_plan(rows, k, n);
+    const int64_t cols = kTile * p.nt * (kWaves / p.wk);
+    const int64_t groups = (n + cols - 1) / cols;
+    while (groups * s < 150 && chunks % (2 * s) == 0 && (chunks / (2 * s)) % p.wk == 0 &&
+           2 * s * mrows <= k / 32)
+      s *= 2;
+    return (int)s;
+  }
+  const int64_t tiles = n / kTile;
   while (chunks % (2 * s) == 0 && chunks / (2 * s) >= kWaves && tiles * 2 * s <= 3072 &&
          2 * s * mrows <= k / 32)
     s *= 2;
@@ -381,12 +573,38 @@ int launch(const SkinnyArgs& a, int splits, hipStream_t s) {
   return launch_status();
 }
 
+template <int MT, int NT, int WK, int D, int EPI>
+int launch_xs(const SkinnyArgs& a, int splits, hipStream_t s) {
+  constexpr int kColsPerBlock = kTile * (EPI == kEpiSiluMul ? NT / 2 : NT) * (kWaves / WK);
+  const int64_t grid_x = (a.n + kColsPerBlock - 1) / kColsPerBlock;
+  hipLaunchKernelGGL((skinny_xs_kernel<MT, NT, WK, D, EPI, true>),
+                     dim3((unsigned)grid_x, (unsigned)splits), dim3(kBlock), 0, s, a);
+  return launch_status();
+}
+
+template <int MT>
+int dispatch_xs_partials(const SkinnyArgs& a, const XsPlan& p, int splits, hipStream_t s) {
+  if (p.wk == 2) return launch_xs<MT, 2, 2, 4, kEpiPartials>(a, splits, s);
+  if (p.d == 4) return launch_xs<MT, 1, 1, 4, kEpiPartials>(a, splits, s);
+  return launch_xs<MT, 1, 1, 6, kEpiPartials>(a, splits, s);
+}
+
 // Tile plans (measured): up to 4 rows of x arrive as one broadcast line per
-// load, so x goes straight into MFMA layout; beyond that x is loaded like W
-// and transposed through LDS.  Larger M shares each x fragment across two
-// n-tiles per wave.
+// load, so x goes straight into MFMA layout; up to 16 x is loaded like W and
+// transposed through LDS by each wave; beyond 16 rows the shared-x kernel
+// stages each x chunk once per workgroup (the plain kernel remains for
+// splits whose chunk count does not divide into the plan's steps).
 int dispatch_partials(const SkinnyArgs& a, int splits, hipStream_t s) {
-  switch ((a.m + kTile - 1) / kTile) {
+  const int mt = (a.m + kTile - 1) / kTile;
+  if (mt > 1) {
+    const XsPlan p = xs_plan(a.m, a.k, a.n);
+    if (a.chunks % p.wk == 0) {
+      if (mt == 2) return dispatch_xs_partials<2>(a, p, splits, s);
+      if (mt == 3) return dispatch_xs_partials<3>(a, p, splits, s);
+      return dispatch_xs_partials<4>(a, p, splits, s);
+    }
+  }
+  switch (mt) {
     case 1:
       if (a.m <= 4) return launch<1, 1, 4, 2, kEpiPartials, true, false>(a, splits, s);
       if (a.n / kTile >= 256) return launch<1, 2, 4, 2, kEpiPartials, true, true>(a, splits, s);
@@ -397,14 +615,16 @@ int dispatch_partials(const SkinnyArgs& a, int splits, hipStream_t s) {
   }
 }
 
+// Gate/up + SiLU: all of K per workgroup; beyond 16 rows one gate and one up
+// tile per wave, four waves sharing each staged x chunk.
 int dispatch_silu(const SkinnyArgs& a, hipStream_t s) {
   switch ((a.m + kTile - 1) / kTile) {
     case 1:
       if (a.m <= 4) return launch<1, 2, 4, 4, kEpiSiluMul, true, false>(a, 1, s);
       return launch<1, 2, 4, 4, kEpiSiluMul, true, true>(a, 1, s);
-    case 2: return launch<2, 2, 4, 2, kEpiSiluMul, true, true>(a, 1, s);
-    case 3: return launch<3, 2, 4, 2, kEpiSiluMul, true, true>(a, 1, s);
-    default: return launch<4, 2, 4, 2, kEpiSiluMul, true, true>(a, 1, s);
+    case 2: return launch_xs<2, 2, 1, 4, kEpiSiluMul>(a, 1, s);
+    case 3: return launch_xs<3, 2, 1, 4, kEpiSiluMul>(a, 1, s);
+    default: return launch_xs<4, 2, 1, 4, kEpiSiluMul>(a, 1, s);
   }
 }
 

@@ -74,7 +74,7 @@ def test_partials_integer_exact_every_path(m):
     n, k = 96, 1024
     x, w = ints((m, k), -4, 4, g), ints((n, k), -3, 3, g)
     xd, wd = x.to(DEV), w.to(DEV)
-    for splits in (1, 2, 4, sk.split_count(n, k, m)):
+    for splits in (1, 2, 4, 16, sk.split_count(n, k, m)):  # 16: one chunk per split
         p = torch.empty((splits, m, n), dtype=torch.float32, device=DEV)
         _lib.call("qf_linear_partials", xd.data_ptr(), m, k, wd.data_ptr(), n, splits,
                   p.data_ptr(), _lib.stream(xd.device))
@@ -82,16 +82,17 @@ def test_partials_integer_exact_every_path(m):
 
 
 @pytest.mark.parametrize("m", [1, 4, 5, 16, 17, 33, 64])
-def test_silu_mul_integer_exact_every_path(m):
-    g = gen(80 + m)
-    n, k = 64, 640
+@pytest.mark.parametrize("n", [64, 96])  # 96: the last workgroup has waves past N
+def test_silu_mul_integer_exact_every_path(m, n):
+    g = gen(80 + m + n)
+    k = 640
     x, gu = ints((m, k), -2, 2, g), ints((2 * n, k), -1, 1, g)
     got = sk.linear_silu_mul(x.to(DEV), gu.to(DEV))
-    assert_bits_exact(got, O.linear_silu_mul(bits(x), bits(gu)), what=f"silu m={m}")
+    assert_bits_exact(got, O.linear_silu_mul(bits(x), bits(gu)), what=f"silu m={m} n={n}")
 
 
 @pytest.mark.parametrize("name", sorted(QWEN))
-@pytest.mark.parametrize("m", [1, 16, 64])
+@pytest.mark.parametrize("m", [1, 16, 32, 48, 64])
 def test_partials_qwen_shapes_integer_exact(name, m):
     n, k = QWEN[name]
     g = gen(100 + m)
@@ -101,7 +102,7 @@ def test_partials_qwen_shapes_integer_exact(name, m):
     torch.testing.assert_close(got.cpu(), exact_int_partials(x, w, got.shape[0]), rtol=0, atol=0)
 
 
-@pytest.mark.parametrize("m", [1, 4, 16, 64])
+@pytest.mark.parametrize("m", [1, 4, 16, 32, 48, 64])
 def test_silu_mul_qwen_shape_integer_exact(m):
     n, k = GATE_UP
     g = gen(120 + m)
