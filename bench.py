@@ -348,8 +348,9 @@ def decode_attention_bench(device, replays: int = 20, calls: int = GRAPH_CALLS) 
     return out
 
 
-#: The engine contract's public workloads (batch, prompt tokens, output tokens).
-ENGINE_WORKLOADS = ((1, 512, 32), (4, 2048, 32), (16, 512, 128))
+#: The engine contract's public workloads (batch, prompt tokens, output tokens),
+#: plus batch 64: the largest batch the split-K decode projections serve.
+ENGINE_WORKLOADS = ((1, 512, 32), (4, 2048, 32), (16, 512, 128), (64, 512, 32))
 
 
 def engine_decode(device, steps: int = 32, workloads=ENGINE_WORKLOADS) -> dict:

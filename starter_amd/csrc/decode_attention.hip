@@ -123,7 +123,7 @@ __device__ __forceinline__ void merge_lanes(State<GT>& s, int mask) {
 }
 
 // One workgroup per (virtual head, key segment), for query rows g0 .. g0+GT-1
-// of the group (those below G); each lane group keeps two sets of U key
+// of the group (those below G); each lane group keeps NS sets of U key
 // blocks (4 keys per wave each) in flight.  With one segment the workgroup
 // writes the output; otherwise it writes its f32 partials and statistics for
 // attn_merge_kernel.
@@ -136,8 +136,9 @@ __device__ __forceinline__ void merge_lanes(State<GT>& s, int mask) {
 // there (first launch of a wide group only) and uses the new rows in place
 // of whatever the slot held when its loads were issued, so no workgroup
 // reads back its own store.
-template <int GT, int U, int W, bool FUSED>
+template <int GT, int U, int W, bool FUSED, int NS = 2>
 __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
+  static_assert(NS >= 2, "at least two sets in flight");
   constexpr int kWavesA = W;
   constexpr int kKeysPerIter = kKeysPerWave * W;  // keys per workgroup step
   static_assert(!FUSED || (W == 4 && GT <= 8), "fused prologue: 16 lane groups, <= 8 query rows");
@@ -189,7 +190,7 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
   const int64_t base0 = start + kKeysPerWave * wave;
   const int n = base0 < end ? (int)((end - base0 + step - 1) / step) : 0;
   const int64_t last_key = end - 1;  // a valid slot whenever n > 0
-  uint4 kv[2][U], vv[2][U];
+  uint4 kv[NS][U], vv[NS][U];
   // Fused: subst marks the segment that attends slot pos, whose new K/V row
   // (this lane's slice) is knew / vnew.
   int64_t pos = 0;
@@ -256,7 +257,10 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
       st.m[g] = mn;
     }
   };
-  if (n > 0) issue(0, 0);
+  if (n > 0) {
+#pragma unroll
+    for (int d = 0; d + 1 < NS; ++d) issue(d, d);
+  }
 
   // Fused prologue (see above).
   if constexpr (FUSED) {
@@ -305,14 +309,20 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
     }
   }
 
+  // NS sets in flight: set t lives in buffer t % NS; before consuming it the
+  // wave issues set t + NS - 1 into the buffer set t - 1 just freed.
   if (n > 0) {
-    for (int i = 0;; i += 2) {
-      issue(1, i + 1);
-      consume(0, i);
-      if (i + 1 >= n) break;
-      issue(0, i + 2);
-      consume(1, i + 1);
-      if (i + 2 >= n) break;
+    for (int i = 0;; i += NS) {
+      bool done = false;
+#pragma unroll
+      for (int d = 0; d < NS; ++d) {
+        if (!done) {
+          issue((d + NS - 1) % NS, i + d + NS - 1);
+          consume(d, i + d);
+          done = i + d + 1 >= n;
+        }
+      }
+      if (done) break;
     }
   }
 
@@ -438,10 +448,13 @@ __global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a, int64_t r
 
 template <int GT, bool FUSED>
 int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
-  // Two sets of U key blocks in flight (U = 4 measured best for up to 4 query
-  // rows; 2 beyond, within the register budget).  Groups wider than GT
-  // (9..16 rows) take two launches of 8 rows each.
-  constexpr int U = GT <= 4 ? 4 : 2;
+  // Two sets of U = 2 key blocks in flight per wave.  Measured on the engine's
+  // workloads (batch x keys = 1 x 545, 4 x 2081, 16 x 641, 64 x 1024): U = 4
+  // is up to 6% slower, U = 8 and three or four sets in flight 10-45%
+  // slower (they only lengthen each wave's chain; the grid already has the
+  // bytes in flight).  Groups wider than GT (9..16 rows) take two launches
+  // of 8 rows each.
+  constexpr int U = 2;
   AttnArgs a = args;
   int st = QF_OK;
   for (a.g0 = 0; a.g0 < a.groups && st == QF_OK; a.g0 += GT) {
