@@ -111,6 +111,7 @@ __device__ __forceinline__ void finish(const SkinnyArgs& a, f32x4 (&acc)[NT][MT]
                                        int lane, int wk, int wn, int col0, bool live, int split) {
   constexpr bool PAIRS = EPI == kEpiSiluMul;
   constexpr int kCols = PAIRS ? NT / 2 : NT;
+  static_assert(EPI != kEpiArgmax || NT == 1, "one argmax candidate per 16-column tile");
   const int r = lane % kTile;
   const int g = lane / kTile;
   // Waves wk = 1..WK-1 of each group hand their tiles to the group's wave
@@ -172,8 +173,8 @@ __device__ __forceinline__ void finish(const SkinnyArgs& a, f32x4 (&acc)[NT][MT]
           besti = oi;
         }
       }
-      if (row_ok && g == 0) {
-        uint2* cand = reinterpret_cast<uint2*>(a.partials) + (int64_t)m * gridDim.x + blockIdx.x;
+      if (row_ok && g == 0) {  // one candidate per row and 16-column tile
+        uint2* cand = reinterpret_cast<uint2*>(a.partials) + (int64_t)m * (a.n / kTile) + col0 / kTile;
         *cand = make_uint2(__float_as_uint(best), (uint32_t)besti);
       }
     }
@@ -675,9 +676,9 @@ int dispatch_argmax(const SkinnyArgs& a, hipStream_t s) {
     case 1:
       if (a.m <= 4) return launch<1, 1, 4, 2, kEpiArgmax, true, false>(a, 1, s);
       return launch<1, 1, 4, 2, kEpiArgmax, true, true>(a, 1, s);
-    case 2: return launch<2, 1, 4, 2, kEpiArgmax, true, true>(a, 1, s);
-    case 3: return launch<3, 1, 4, 2, kEpiArgmax, true, true>(a, 1, s);
-    default: return launch<4, 1, 4, 2, kEpiArgmax, true, true>(a, 1, s);
+    case 2: return launch_xs<2, 1, 1, 4, kEpiArgmax>(a, 1, s);
+    case 3: return launch_xs<3, 1, 1, 4, kEpiArgmax>(a, 1, s);
+    default: return launch_xs<4, 1, 1, 4, kEpiArgmax>(a, 1, s);
   }
 }
 

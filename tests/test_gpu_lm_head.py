@@ -26,12 +26,13 @@ DEV = "cuda"
 
 
 @pytest.mark.parametrize("m", [1, 3, 4, 5, 16, 17, 33, 64])
-def test_integer_logits_and_tied_tokens_exact(m):
-    g = gen(600 + m)
+@pytest.mark.parametrize("vocab", [4096, 4112])  # 4112: a partly filled last workgroup
+def test_integer_logits_and_tied_tokens_exact(m, vocab):
+    g = gen(600 + m + vocab)
     x = torch.zeros(m, 256, dtype=torch.bfloat16)
     x[:, 0] = 1
     x[:, 1:4] = torch.randint(0, 2, (m, 3), generator=g).to(torch.bfloat16)
-    w = torch.randint(-1, 2, (4096, 256), generator=g).to(torch.bfloat16)
+    w = torch.randint(-1, 2, (vocab, 256), generator=g).to(torch.bfloat16)
     tokens, logits = lm_head_argmax(x.to(DEV), w.to(DEV), logits=True)
     ref_tokens, ref_logits = O.lm_head_argmax(bits(x), bits(w))
     assert_bits_exact(logits, ref_logits, what="logits")
