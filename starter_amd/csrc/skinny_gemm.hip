@@ -542,7 +542,9 @@ XsPlan xs_plan(int64_t rows, int64_t k, int64_t n) {
 // Power-of-two K splits (measured on the Qwen3-4B projection shapes).  Up to
 // 16 rows: as many as keep every wave at least one chunk, the grid at most
 // 3072 workgroups of 16 columns (~12 per CU), and the partials (written here,
-// read by the consumer) small: splits * min(M, 16) <= K / 32.  Beyond 16 rows
+// read by the consumer) small: splits * min(M, 16) <= K / 32, at most 8 (o_proj
+// takes the same time at 8 and 16 splits, and its consumer, one workgroup per
+// row, reads half the bytes).  Beyond 16 rows
 // (shared-x kernel): the fewest that give ~150 workgroups, within the same
 // partials bound and whole steps per split.
 int plan_splits(int64_t rows, int64_t k, int64_t n) {
@@ -559,7 +561,7 @@ int plan_splits(int64_t rows, int64_t k, int64_t n) {
     return (int)s;
   }
   const int64_t tiles = n / kTile;
-  while (chunks % (2 * s) == 0 && chunks / (2 * s) >= kWaves && tiles * 2 * s <= 3072 &&
+  while (s < 8 && chunks % (2 * s) == 0 && chunks / (2 * s) >= kWaves && tiles * 2 * s <= 3072 &&
          2 * s * mrows <= k / 32)
     s *= 2;
   return (int)s;

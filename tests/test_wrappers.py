@@ -332,7 +332,7 @@ def test_skinny_split_plan():
             assert prev is None or s <= prev
             prev = s
     assert sk.split_count(6144, 2560, 1) == 8 and sk.split_count(6144, 2560, 16) == 4
-    assert sk.split_count(2560, 4096, 1) == 16 and sk.split_count(2560, 9728, 16) == 8
+    assert sk.split_count(2560, 4096, 1) == 8 and sk.split_count(2560, 9728, 16) == 8
     # beyond 16 rows (shared-x kernel): the fewest splits giving ~150 workgroups
     assert [sk.split_count(n, k, 64) for n, k in qwen.values()] == [2, 4, 4]
     assert sk.split_count(6144, 2560, 32) == 2 and sk.split_count(2560, 4096, 48) == 4
