@@ -495,7 +495,7 @@ def profile_run(device, launches: int) -> None:
     """Eager launches for counter collection: a calibration copy of known size
     (CALIBRATION_BYTES read + written by torch's copy kernel), then each
     prefill kernel ``launches`` times on rotating buffer sets, then each decode
-    projection at batch 1 and 16 ``launches`` times on rotating weights."""
+    projection at batch 1, 16 and 64 ``launches`` times on rotating weights."""
     src = torch.empty(CALIBRATION_BYTES // 2, dtype=BF16, device=device).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -510,14 +510,14 @@ def profile_run(device, launches: int) -> None:
         torch.cuda.synchronize()
     del work
     torch.cuda.empty_cache()
-    # Decode projections at batch 1 and 16, in this order (dispatch order
+    # Decode projections at batch 1, 16 and 64, in this order (dispatch order
     # tells apart projections that share a kernel instantiation).
     g = torch.Generator(device=device).manual_seed(1)
     order = []
     for name, (n, k) in PROJECTIONS.items():
         rows_w = 2 * n if name == "gate_up" else n
         weights = [normal((rows_w, k), 0.0, k ** -0.5, g) for _ in range(sets_for(bf16_bytes(rows_w * k)))]
-        for m in (1, 16):
+        for m in (1, 16, 64):
             x = normal((m, k), g=g)
             fn = skinny_gemm.linear_silu_mul if name == "gate_up" else skinny_gemm.linear_partials
             for i in range(launches):
