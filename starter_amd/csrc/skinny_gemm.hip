@@ -63,7 +63,7 @@ constexpr int kColAlign = 32;  // N granularity of the shape rule
 // Epilogues.
 constexpr int kEpiPartials = 0;  // f32 split-K partials [S, M, N]
 constexpr int kEpiSiluMul = 1;   // packed gate/up -> bf16 silu(gate) * up [M, N]
-constexpr int kEpiArgmax = 2;    // bf16 logits (optional) + per-workgroup argmax candidates
+constexpr int kEpiArgmax = 2;    // bf16 logits (optional) + argmax candidates per 16-column tile
 
 // Is (v, i) ahead of (bv, bi) in argmax order: larger value, NaN above
 // everything, the lower index on equal values (torch.argmax's first maximum)?
@@ -111,7 +111,6 @@ __device__ __forceinline__ void finish(const SkinnyArgs& a, f32x4 (&acc)[NT][MT]
                                        int lane, int wk, int wn, int col0, bool live, int split) {
   constexpr bool PAIRS = EPI == kEpiSiluMul;
   constexpr int kCols = PAIRS ? NT / 2 : NT;
-  static_assert(EPI != kEpiArgmax || NT == 1, "one argmax candidate per 16-column tile");
   const int r = lane % kTile;
   const int g = lane / kTile;
   // Waves wk = 1..WK-1 of each group hand their tiles to the group's wave
@@ -139,17 +138,18 @@ __device__ __forceinline__ void finish(const SkinnyArgs& a, f32x4 (&acc)[NT][MT]
   }
 
   if constexpr (EPI == kEpiArgmax) {
-    // bf16 logits of this workgroup's 16*NT columns; per row the largest,
-    // lowest column on ties (NaN counts as largest), reduced over the four
-    // lanes that hold a row (all lanes take part in the shuffles).
+    // bf16 logits of this wave's 16*NT columns; per row and 16-column tile
+    // the largest, lowest column on ties (NaN counts as largest), reduced
+    // over the four lanes that hold a row of the tile (all lanes take part in
+    // the shuffles); one candidate per row and tile.
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int m = kTile * mt + r;
       const bool row_ok = live && m < a.m;
-      float best = -__builtin_inff();
-      int besti = INT32_MAX;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
+        float best = -__builtin_inff();
+        int besti = INT32_MAX;
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -163,19 +163,20 @@ __device__ __forceinline__ void finish(const SkinnyArgs& a, f32x4 (&acc)[NT][MT]
         if (row_ok && a.out)
           *reinterpret_cast<uint2*>(a.out + (int64_t)m * a.n + col0 + kTile * t + 4 * g) =
               make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
-      }
 #pragma unroll
-      for (int mask = 16; mask <= 32; mask *= 2) {
-        const float ov = __shfl_xor(best, mask);
-        const int oi = __shfl_xor(besti, mask);
-        if (better(ov, oi, best, besti)) {
-          best = ov;
-          besti = oi;
+        for (int mask = 16; mask <= 32; mask *= 2) {
+          const float ov = __shfl_xor(best, mask);
+          const int oi = __shfl_xor(besti, mask);
+          if (better(ov, oi, best, besti)) {
+            best = ov;
+            besti = oi;
+          }
         }
-      }
-      if (row_ok && g == 0) {  // one candidate per row and 16-column tile
-        uint2* cand = reinterpret_cast<uint2*>(a.partials) + (int64_t)m * (a.n / kTile) + col0 / kTile;
-        *cand = make_uint2(__float_as_uint(best), (uint32_t)besti);
+        if (row_ok && g == 0) {
+          uint2* cand = reinterpret_cast<uint2*>(a.partials) + (int64_t)m * (a.n / kTile) +
+                        col0 / kTile + t;
+          *cand = make_uint2(__float_as_uint(best), (uint32_t)besti);
+        }
       }
     }
     return;
@@ -673,11 +674,21 @@ __global__ __launch_bounds__(kBlock) void argmax_finalize_kernel(const uint2* ca
   }
 }
 
+// LM head plans (measured on the Qwen3-4B head, 151936 x 2560, at 1, 4, 8 and
+// 16 rows): up to 4 rows x straight into MFMA layout with four chunks in
+// flight (two n-tiles per wave from 2 rows); 5..16 rows the shared-x kernel
+// with two n-tiles per wave and wave pairs splitting K (20% faster at 16
+// rows than per-wave x staging).  Two-tile plans need vocab % 32 == 0.
 int dispatch_argmax(const SkinnyArgs& a, hipStream_t s) {
+  const bool two = a.n % (2 * kTile) == 0;
   switch ((a.m + kTile - 1) / kTile) {
     case 1:
-      if (a.m <= 4) return launch<1, 1, 4, 2, kEpiArgmax, true, false>(a, 1, s);
-      return launch<1, 1, 4, 2, kEpiArgmax, true, true>(a, 1, s);
+      if (a.m == 1 || !two) {
+        if (a.m <= 4) return launch<1, 1, 4, 4, kEpiArgmax, true, false>(a, 1, s);
+        return launch_xs<1, 1, 1, 4, kEpiArgmax>(a, 1, s);
+      }
+      if (a.m <= 4) return launch<1, 2, 4, 4, kEpiArgmax, true, false>(a, 1, s);
+      return launch_xs<1, 2, 2, 4, kEpiArgmax>(a, 1, s);
     case 2: return launch_xs<2, 1, 1, 4, kEpiArgmax>(a, 1, s);
     case 3: return launch_xs<3, 1, 1, 4, kEpiArgmax>(a, 1, s);
     default: return launch_xs<4, 1, 1, 4, kEpiArgmax>(a, 1, s);
