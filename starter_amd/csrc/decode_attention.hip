@@ -15,6 +15,10 @@
 // second small kernel; only the merged result is rounded to bf16.  Keys at or beyond used[vh] are never loaded, so stale
 // values (NaN poison included) in unused cache slots stay invisible.
 //
+// Groups of up to 4 query rows (Qwen3-4B's 4) take attn_mfma_kernel, which
+// computes the scores on the matrix cores (see there); wider groups take
+// attn_kernel, all on the VALU.
+//
 // Layout (HBM-bound: every K/V byte of the used prefix is read once, ~4
 // flops per byte): a wave reads 4 consecutive keys per 16-byte load - 16
 // lanes per 256-byte key row, lane r holding d = 8r .. 8r+8 - so every load
@@ -120,6 +124,57 @@ __device__ __forceinline__ void merge_lanes(State<GT>& s, int mask) {
     for (int j = 0; j < 8; ++j) oacc[j] = __shfl_xor(s.acc[g][j], mask);
     merge_row<GT>(s, g, om, ol, oacc);
   }
+}
+
+// Fused Q/K/V prologue (qf_decode_attention_qkv), run by every lane of the
+// workgroup before the key loop: lane group lg (16 lanes = one DPP row, lane
+// r holding elements 8r..8r+8) folds or loads one packed row of virtual head
+// vh - query rows g0 + lg for lg < rows, the new key row for lg == 8, the new
+// value row for lg == 9 - and writes the normalised, rotated queries to
+// qs[lg] and the new K / V rows to kvs[0] / kvs[1] (LDS; the caller
+// synchronises before reading them).  The segment starting at `start` that
+// owns slot `pos` also stores the new K / V row into the caches (first
+// launch of a wide group only).  A position outside the cache gives NaN
+// queries and writes nothing, as qf_qkv_norm_rope_cache does.  Returns
+// whether this segment owns the slot.
+__device__ __forceinline__ bool fused_prologue(const AttnArgs& a, int vh, int lg, int r, int rows,
+                                               int64_t start, int64_t pos, uint4 (*qs)[16],
+                                               uint4 (*kvs)[16]) {
+  const int G = a.groups;
+  const int64_t hkv = a.kv_heads;
+  const int64_t b = vh / hkv, h = vh - b * hkv;
+  const int64_t hq = hkv * G;
+  const int64_t width = (hq + 2 * hkv) * kD;
+  const bool pos_ok = pos >= 0 && pos < a.capacity;
+  const int64_t slot = pos_ok ? pos : 0;
+  const bool is_q = lg < rows, is_k = lg == 8, is_v = lg == 9;
+  const bool live = is_q || is_k || is_v;
+  const int64_t head = is_q ? h * G + a.g0 + lg : is_k ? hq + h : hq + hkv + h;
+  const int64_t off = b * width + head * kD + 8 * r;
+  // Gains and rotary rows first: the fold below waits for its loads, and
+  // these should already be in flight by then.
+  const uint4 wv = load16<false>((is_q ? a.qw : a.kw) + 8 * r);
+  const uint4 cv = load16<false>(a.cos + slot * kD + 8 * r);
+  const uint4 sv = load16<false>(a.sin + slot * kD + 8 * r);
+  float x[8];
+  uint4 xv;
+  if (a.qkv_splits == 0) {
+    xv = live ? load16<false>(static_cast<const uint16_t*>(a.qkv) + off) : make_uint4(0, 0, 0, 0);
+  } else {
+    sum_partials8<8>(static_cast<const float*>(a.qkv) + off, a.qkv_stride, a.qkv_splits, live, x);
+    xv = pack8(x);  // one rounding of the f32 sum
+  }
+  unpack8(xv, x);
+  const uint4 o = norm_rope(x, wv, cv, sv, is_q ? a.q_eps : a.k_eps, r);  // every lane: DPP
+  const uint4 nan4 = make_uint4(0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u);
+  if (is_q) qs[lg][r] = select4(pos_ok, o, nan4);
+  if (is_k) kvs[0][r] = o;
+  if (is_v) kvs[1][r] = xv;
+  const bool owns_slot = pos_ok && pos >= start && pos < start + a.span;
+  if (owns_slot && a.g0 == 0 && (is_k || is_v))
+    store16<false>((is_k ? a.kc : a.vc) + ((int64_t)vh * a.capacity + pos) * kD + 8 * r,
+                   select4(is_k, o, xv));
+  return owns_slot;
 }
 
 // One workgroup per (virtual head, key segment), for query rows g0 .. g0+GT-1
@@ -264,41 +319,8 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
 
   // Fused prologue (see above).
   if constexpr (FUSED) {
-    const int lg = wave * 4 + q4;  // lane group 0..15, one DPP row each
-    const int64_t hkv = a.kv_heads;
-    const int64_t b = vh / hkv, h = vh - b * hkv;
-    const int64_t hq = hkv * G;
-    const int64_t width = (hq + 2 * hkv) * kD;
     pos = pos_in;
-    const bool pos_ok = pos >= 0 && pos < a.capacity;
-    const int64_t slot = pos_ok ? pos : 0;
-    const bool is_q = lg < rows, is_k = lg == 8, is_v = lg == 9;
-    const bool live = is_q || is_k || is_v;
-    const int64_t head = is_q ? h * G + a.g0 + lg : is_k ? hq + h : hq + hkv + h;
-    const int64_t off = b * width + head * kD + 8 * r;
-    // Gains and rotary rows first: the fold below waits for its loads, and
-    // these should already be in flight by then.
-    const uint4 wv = load16<false>((is_q ? a.qw : a.kw) + 8 * r);
-    const uint4 cv = load16<false>(a.cos + slot * kD + 8 * r);
-    const uint4 sv = load16<false>(a.sin + slot * kD + 8 * r);
-    float x[8];
-    uint4 xv;
-    if (a.qkv_splits == 0) {
-      xv = live ? load16<false>(static_cast<const uint16_t*>(a.qkv) + off) : make_uint4(0, 0, 0, 0);
-    } else {
-      sum_partials8<8>(static_cast<const float*>(a.qkv) + off, a.qkv_stride, a.qkv_splits, live, x);
-      xv = pack8(x);  // one rounding of the f32 sum
-    }
-    unpack8(xv, x);
-    const uint4 o = norm_rope(x, wv, cv, sv, is_q ? a.q_eps : a.k_eps, r);  // every lane: DPP
-    const uint4 nan4 = make_uint4(0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u);
-    if (is_q) qs[lg][r] = select4(pos_ok, o, nan4);
-    if (is_k) kvs[0][r] = o;
-    if (is_v) kvs[1][r] = xv;
-    const bool owns_slot = pos_ok && pos >= start && pos < start + a.span;
-    if (owns_slot && a.g0 == 0 && (is_k || is_v))
-      store16<false>((is_k ? a.kc : a.vc) + ((int64_t)vh * a.capacity + pos) * kD + 8 * r,
-                     select4(is_k, o, xv));
+    const bool owns_slot = fused_prologue(a, vh, wave * 4 + q4, r, rows, start, pos, qs, kvs);
     __syncthreads();
 #pragma unroll
     for (int g = 0; g < GT; ++g) qv[g] = g < rows ? qs[g][r] : make_uint4(0, 0, 0, 0);
@@ -386,6 +408,261 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
   }
 }
 
+// Matrix-core variant for groups of at most 4 query rows (Qwen3: 4), the
+// same contract and results within the kernels' bf16 rounding of the
+// probabilities.  Each wave takes 16-key blocks w, w+4, ... of the segment:
+// S = Q K^T of a block is one chain of four v_mfma_f32_16x16x32_bf16 (A = the
+// query rows, zero-padded to 16; B = the 16 keys, lane l reading key l % 16,
+// dims 8*(l/16) + 32s, straight from the cache), which leaves S[q][key] in
+// lanes 0..15.  The wave keeps one running maximum per query (a 16-lane DPP
+// maximum per block), so its four lane groups can later be summed without
+// rescaling; the bf16 probabilities reach the PV layout (lane group per key,
+// lane r holding dims 8r..8r+8, as in attn_kernel) through ds_bpermute, and
+// PV stays f32 FMAs.  Compared with attn_kernel this removes the per-key dot
+// products and their 16-lane sums from the VALU.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float dpp_max16(float x) {
+  x = fmaxf(x, __uint_as_float(dpp_u32<kQuadXor1>(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(dpp_u32<kQuadXor2>(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(dpp_u32<kRowHalfMirror>(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(dpp_u32<kRowMirror>(__float_as_uint(x))));
+  return x;
+}
+// Lane 0's value in every lane (all lanes active).
+__device__ __forceinline__ float first_lane(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
+
+template <int GT, bool FUSED, int NS = 2>
+__global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
+  static_assert(GT == 1 || GT == 2 || GT == 4, "query rows per kv head");
+  constexpr int kW = kBlock / kWave;
+  __shared__ float xm[kW - 1][GT], xl[kW - 1][GT];
+  __shared__ float xacc[kW - 1][GT][kD];
+  __shared__ uint4 qs[FUSED ? GT : 1][16], kvs[2][16];
+  const int vh = blockIdx.x;
+  const int seg = blockIdx.y;
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int r = lane % 16;
+  const int q4 = lane / 16;
+  const int G = a.groups;  // <= GT
+  const int rows = G;
+
+  const int32_t used_in = a.used[vh];
+  const int64_t pos_in = FUSED ? *a.position : 0;
+  if constexpr (FUSED) asm volatile("" ::"s"(used_in), "s"(pos_in));
+  int64_t used = used_in;
+  used = used < 0 ? 0 : (used > a.capacity ? a.capacity : used);
+  const int64_t start = (int64_t)seg * a.span;
+  int64_t end = start + a.span;
+  if (end > used) end = used;
+  const uint16_t* kbase = a.k + (int64_t)vh * a.capacity * kD;
+  const uint16_t* vbase = a.v + (int64_t)vh * a.capacity * kD;
+  const int64_t nb = end > start ? (end - start + 15) / 16 : 0;  // 16-key blocks of the segment
+  const int n = nb > wave ? (int)((nb - wave + kW - 1) / kW) : 0;
+  const int64_t last_key = end - 1;  // a valid slot whenever n > 0
+
+  // Query rows as the MFMA A operand: row = lane % 16 (< G), k = dims 8*(lane/16) + 32 s.
+  uint4 qa[4];
+  if constexpr (!FUSED) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qa[s] = r < rows ? load16<false>(a.q + ((int64_t)vh * G + r) * kD + 8 * q4 + 32 * s)
+                       : make_uint4(0, 0, 0, 0);
+  }
+
+  uint4 kf[NS][4], vf[NS][4];
+  int64_t pos = 0;
+  bool subst = false;
+  uint4 knew[4], vnew = make_uint4(0, 0, 0, 0);
+  auto issue = [&](int d, int j) {
+    const int64_t b0 = start + (int64_t)(wave + kW * j) * 16;
+    const int64_t kk = b0 + r < end ? b0 + r : last_key;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kf[d][s] = load16<false>(kbase + kk * kD + 8 * q4 + 32 * s);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t vk = b0 + q4 + 4 * u < end ? b0 + q4 + 4 * u : last_key;
+      vf[d][u] = load16<false>(vbase + vk * kD + 8 * r);
+    }
+  };
+  if (n > 0) {
+#pragma unroll
+    for (int d = 0; d + 1 < NS; ++d) issue(d, d);
+  }
+  if constexpr (FUSED) {
+    pos = pos_in;
+    const bool owns_slot = fused_prologue(a, vh, wave * 4 + q4, r, rows, start, pos, qs, kvs);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qa[s] = r < rows ? qs[r][q4 + 4 * s] : make_uint4(0, 0, 0, 0);
+    subst = owns_slot && pos < end;
+    if (subst) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) knew[s] = kvs[0][q4 + 4 * s];
+      vnew = kvs[1][r];
+    }
+  }
+
+  float m[GT], l[GT], acc[GT][8];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    m[g] = kNegInf;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
+  }
+  auto consume = [&](int d, int j) {
+    const int64_t b0 = start + (int64_t)(wave + kW * j) * 16;
+    if constexpr (FUSED) {
+      if (subst) {  // the new K/V row replaces slot pos wherever it was loaded
+        if ((b0 + r < end ? b0 + r : last_key) == pos) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) kf[d][s] = knew[s];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if ((b0 + q4 + 4 * u < end ? b0 + q4 + 4 * u : last_key) == pos) vf[d][u] = vnew;
+      }
+    }
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[s]),
+                                                   __builtin_bit_cast(bf16x8, kf[d][s]), c, 0, 0, 0);
+    // Lanes 0..15 hold S[q = i][key b0 + lane]; other rows are padding.
+    const bool on = b0 + r < end;
+    float sc[GT], mn[GT], corr[GT];
+    bool rescale = false;
+#pragma unroll
+    for (int i = 0; i < GT; ++i) {
+      sc[i] = on ? c[i] * a.scale_log2 : kNegInf;
+      mn[i] = fmaxf(m[i], first_lane(dpp_max16(sc[i])));
+      corr[i] = mn[i] == kNegInf ? 1.0f : exp2_hw(m[i] - mn[i]);
+      rescale |= corr[i] != 1.0f;
+    }
+    if (rescale) {  // wave-uniform
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        l[g] *= corr[g];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) acc[g][jj] *= corr[g];
+      }
+    }
+    float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < GT; ++i) {
+      p[i] = mn[i] == kNegInf ? 0.0f : exp2_hw(sc[i] - mn[i]);  // 0 for a masked key
+      l[i] += p[i];  // partial over this lane's keys (lanes 0..15 count)
+      m[i] = mn[i];
+    }
+    const uint32_t p01 = pack2(p[0], p[1]), p23 = pack2(p[2], p[3]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int src = (q4 + 4 * u) * 4;  // byte address of the lane holding key q4 + 4u
+      const uint32_t b01 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)p01);
+      uint32_t b23 = 0;
+      if constexpr (GT == 4) b23 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)p23);
+      const float pg[4] = {lo_f32(b01), hi_f32(b01), lo_f32(b23), hi_f32(b23)};
+      float v[8];
+      unpack8(vf[d][u], v);
+#pragma unroll
+      for (int g = 0; g < GT; ++g)
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) acc[g][jj] = __builtin_fmaf(pg[g], v[jj], acc[g][jj]);
+    }
+  };
+  if (n > 0) {
+    for (int i = 0;; i += NS) {
+      bool done = false;
+#pragma unroll
+      for (int d = 0; d < NS; ++d) {
+        if (!done) {
+          issue((d + NS - 1) % NS, i + d + NS - 1);
+          consume(d, i + d);
+          done = i + d + 1 >= n;
+        }
+      }
+      if (done) break;
+    }
+  }
+
+  // Wave totals (one maximum per wave): l over the 16 key lanes of row 0,
+  // acc over the four lane groups.
+  State<GT> st;
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    float t = l[g];
+    t += __uint_as_float(dpp_u32<kQuadXor1>(__float_as_uint(t)));
+    t += __uint_as_float(dpp_u32<kQuadXor2>(__float_as_uint(t)));
+    t += __uint_as_float(dpp_u32<kRowHalfMirror>(__float_as_uint(t)));
+    t += __uint_as_float(dpp_u32<kRowMirror>(__float_as_uint(t)));
+    st.l[g] = first_lane(t);
+    st.m[g] = m[g];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      float v = acc[g][jj];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      st.acc[g][jj] = v;
+    }
+  }
+  if (wave > 0 && lane < 16) {
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (lane == 0) {
+        xm[wave - 1][g] = st.m[g];
+        xl[wave - 1][g] = st.l[g];
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) xacc[wave - 1][g][8 * r + jj] = st.acc[g][jj];
+    }
+  }
+  __syncthreads();
+  const bool owner = wave == 0 && lane < 16;
+  if (owner) {
+#pragma unroll
+    for (int w = 0; w < kW - 1; ++w)
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        float oacc[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) oacc[jj] = xacc[w][g][8 * r + jj];
+        merge_row<GT>(st, g, xm[w][g], xl[w][g], oacc);
+      }
+  }
+  if (a.splits == 1) {
+    if (!owner) return;
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (g >= rows) break;
+      const float den = st.l[g] > 0.0f ? st.l[g] : 1.0f;
+      float o[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) o[jj] = st.acc[g][jj] / den;
+      store16<false>(a.out + ((int64_t)vh * G + g) * kD + 8 * r, pack8(o));
+    }
+    return;
+  }
+  if (owner) {
+    const int64_t slot = (int64_t)vh * a.splits + seg;
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (g >= rows) break;
+      float* dst = a.partials + (slot * G + g) * kD + 8 * r;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) dst[jj] = st.acc[g][jj];
+      if (r == 0) {
+        a.stats[slot * 2 * G + g] = st.m[g];
+        a.stats[slot * 2 * G + G + g] = st.l[g];
+      }
+    }
+  }
+}
+
 // One 16-lane group per query row (4 rows per wave): weights 2^(m_s - M)
 // for segments with a positive denominator, summed in segment order.  All
 // statistics, then the partials in groups of 16 segments, are loaded before
@@ -457,10 +734,16 @@ int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
   constexpr int U = 2;
   AttnArgs a = args;
   int st = QF_OK;
-  for (a.g0 = 0; a.g0 < a.groups && st == QF_OK; a.g0 += GT) {
-    hipLaunchKernelGGL((attn_kernel<GT, U, 4, FUSED>), dim3((unsigned)vheads, (unsigned)a.splits),
+  if constexpr (GT <= 4) {  // one launch: Q.K^T on the matrix cores
+    hipLaunchKernelGGL((attn_mfma_kernel<GT, FUSED>), dim3((unsigned)vheads, (unsigned)a.splits),
                        dim3(kBlock), 0, s, a);
     st = launch_status();
+  } else {
+    for (a.g0 = 0; a.g0 < a.groups && st == QF_OK; a.g0 += GT) {
+      hipLaunchKernelGGL((attn_kernel<GT, U, 4, FUSED>), dim3((unsigned)vheads, (unsigned)a.splits),
+                         dim3(kBlock), 0, s, a);
+      st = launch_status();
+    }
   }
   if (st != QF_OK || a.splits == 1) return st;
   const int64_t rows = vheads * a.groups;
