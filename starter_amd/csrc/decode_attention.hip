@@ -12,12 +12,13 @@
 // maximum grows; the probabilities that multiply V are rounded to bf16 first
 // (as the reference feeds them to a bf16 dot) while l sums them in f32.
 // Segments are merged with weights 2^(m_s - M), in segment order, by a
-// second small kernel; only the merged result is rounded to bf16.  Keys at or beyond used[vh] are never loaded, so stale
-// values (NaN poison included) in unused cache slots stay invisible.
+// second small kernel; only the merged result is rounded to bf16.  Keys at
+// or beyond used[vh] are never loaded, so stale values (NaN poison included)
+// in unused cache slots stay invisible.
 //
 // Groups of up to 4 query rows (Qwen3-4B's 4) take attn_mfma_kernel, which
 // computes the scores on the matrix cores (see there); wider groups take
-// attn_kernel, all on the VALU.
+// attn_kernel, all on the VALU, described next.
 //
 // Layout (HBM-bound: every K/V byte of the used prefix is read once, ~4
 // flops per byte): a wave reads 4 consecutive keys per 16-byte load - 16
