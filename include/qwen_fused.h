@@ -186,6 +186,29 @@ int qf_linear_partials(const void* x, int64_t rows, int64_t k, const void* weigh
                        int64_t n, int32_t splits, void* partials, void* stream);
 
 /*
+ * qf_linear_partials of the attention output, taken from the unmerged
+ * segments of qf_decode_attention / qf_decode_attention_qkv (called with
+ * out = NULL): x = the merge those calls would have written, bf16
+ * [batch, q_heads * 128], k = q_heads * 128.  Each projection workgroup
+ * merges the heads of its own K range into LDS while its first weight
+ * chunks are in flight, so the attention needs no merge launch and x never
+ * goes to memory.  seg_partials / seg_stats / seg_splits (>= 2) are the
+ * attention's scratch and splits; 1 <= batch <= 16; splits must divide
+ * k / 64 into an even number of chunks (whole heads per split), and
+ * batch * (k / splits * 2 + 16) bytes must fit 64 KiB (QF_E_ARG /
+ * QF_E_SHAPE otherwise).  Bit-identical to the attention's merge followed
+ * by qf_linear_partials with the same splits.
+ * Replaces the hand-off engine/decode_step.py:48-52 makes from the
+ * attention's merged output (the _merge kernel of
+ * engine/kernels/small_query_attention.py:88-110) to linear_partials for
+ * o_proj (engine/kernels/skinny_gemm.py:100-109).
+ */
+int qf_linear_partials_merged(const float* seg_partials, const float* seg_stats,
+                              int32_t seg_splits, int64_t batch, int32_t q_heads,
+                              int32_t kv_heads, const void* weight, int64_t n, int32_t splits,
+                              void* partials, void* stream);
+
+/*
  * Decode gate/up projection with the SiLU * up epilogue, for a packed
  * weight gate_up bf16 [2n, k] (gate rows first):
  *   g = bf16(x @ gate^T),  u = bf16(x @ up^T)     (f32 accumulation, as above)
@@ -223,7 +246,9 @@ int qf_attention_partition(int64_t virtual_heads, int64_t capacity, int32_t comp
  * needs scratch: partials f32 [batch*kv_heads, splits, G, 128] and stats f32
  * [batch*kv_heads, splits, 2, G] (G = q_heads / kv_heads); calls sharing it
  * must be ordered on one stream.  One launch per 8 query rows of a group
- * (one for Qwen3's G = 4), plus a merge launch when splits > 1.
+ * (one for Qwen3's G = 4), plus a merge launch when splits > 1.  With
+ * splits > 1, out may be NULL: the merge launch is skipped and the unmerged
+ * segments stay in partials/stats for qf_linear_partials_merged.
  * Replaces SmallQueryAttention.run + _segments + _merge
  * (engine/kernels/small_query_attention.py:41-110, 135-158).
  */

@@ -29,6 +29,7 @@
 // the segment, each with its own running state, and are merged in lane-group
 // then wave order at the end.
 #include "qf_device.h"
+#include "qf_merge.h"
 #include "qf_rope.h"
 
 namespace qf {
@@ -40,7 +41,7 @@ constexpr int kD = 128;
 constexpr int kKeysPerWave = 4;                       // one 1 KiB load = 4 key rows
 constexpr int kSpanAlign = 16;                        // segment lengths are multiples of 16
 constexpr int kMaxGroups = 16;
-constexpr int kMaxSplits = 32;
+constexpr int kMaxSplits = kMaxSegments;
 constexpr float kNegInf = -__builtin_inff();
 
 struct AttnArgs {
@@ -664,64 +665,17 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
   }
 }
 
-// One 16-lane group per query row (4 rows per wave): weights 2^(m_s - M)
-// for segments with a positive denominator, summed in segment order.  All
-// statistics, then the partials in groups of 16 segments, are loaded before
-// they are combined, so the kernel waits one or two memory latencies, not S.
-constexpr int kMergeBatch = 16;
-__global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a, int64_t rows) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 16;
-  const int r = threadIdx.x % 16;
+// One wave per query row, four rows per workgroup.
+constexpr int kMergeRows = kBlock / kWave;
+__global__ __launch_bounds__(kBlock) void attn_merge_kernel(AttnArgs a, int64_t rows) {
+  const int64_t row = (int64_t)blockIdx.x * kMergeRows + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
   const int G = a.groups;
   const int64_t vh = row / G;
   const int g = (int)(row - vh * G);
-  const int S = a.splits;
-  const float* stats = a.stats + vh * S * 2 * G;
-  float m[kMaxSplits], l[kMaxSplits];
-#pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) {
-    m[s] = kNegInf;
-    l[s] = 0.0f;
-    if (s < S) {
-      m[s] = stats[s * 2 * G + g];
-      l[s] = stats[s * 2 * G + G + g];
-    }
-  }
-  float M = kNegInf;
-#pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) M = fmaxf(M, m[s]);
-  if (M == kNegInf) M = 0.0f;
-  float total = 0.0f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  const float* base = a.partials + (vh * S * G + g) * kD + 8 * r;
-#pragma unroll
-  for (int s0 = 0; s0 < kMaxSplits; s0 += kMergeBatch) {
-    if (s0 >= S) break;
-    float4 lo[kMergeBatch], hi[kMergeBatch];
-#pragma unroll
-    for (int i = 0; i < kMergeBatch; ++i) {
-      lo[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      hi[i] = lo[i];
-      if (s0 + i < S) {
-        const float4* p = reinterpret_cast<const float4*>(base + (int64_t)(s0 + i) * G * kD);
-        lo[i] = p[0];
-        hi[i] = p[1];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kMergeBatch; ++i) {
-      if (s0 + i < S) {
-        const float w = l[s0 + i] > 0.0f ? exp2_hw(m[s0 + i] - M) : 0.0f;
-        total += l[s0 + i] * w;
-        acc[0] += lo[i].x * w; acc[1] += lo[i].y * w; acc[2] += lo[i].z * w; acc[3] += lo[i].w * w;
-        acc[4] += hi[i].x * w; acc[5] += hi[i].y * w; acc[6] += hi[i].z * w; acc[7] += hi[i].w * w;
-      }
-    }
-  }
-  const float den = total > 0.0f ? total : 1.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] /= den;
-  store16<false>(a.out + row * kD + 8 * r, pack8(acc));
+  reinterpret_cast<uint32_t*>(a.out + row * kD)[lane] =
+      merge_segments_row(a.partials, a.stats, vh, a.splits, G, g, lane);
 }
 
 template <int GT, bool FUSED>
@@ -746,9 +700,10 @@ int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
       st = launch_status();
     }
   }
-  if (st != QF_OK || a.splits == 1) return st;
+  if (st != QF_OK || a.splits == 1 || !a.out) return st;  // no out: segments stay unmerged
   const int64_t rows = vheads * a.groups;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(kWave), 0, s, a, rows);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)((rows + kMergeRows - 1) / kMergeRows)), dim3(kBlock), 0,
+                     s, a, rows);
   return launch_status();
 }
 
@@ -786,7 +741,7 @@ int attention_setup(const void* qsrc, const void* k, const void* v, const int32_
                     void* out, AttnArgs& a, int64_t& vheads) {
   if (batch < 1 || q_heads < 1 || kv_heads < 1 || capacity < 1) return QF_E_ARG;
   if (q_heads % kv_heads != 0 || q_heads / kv_heads > kMaxGroups) return QF_E_SHAPE;
-  if (!qsrc || !k || !v || !used || !out) return QF_E_ARG;
+  if (!qsrc || !k || !v || !used || (!out && splits == 1)) return QF_E_ARG;
   if (splits < 1 || splits > kMaxSplits || span < 1 || span % kSpanAlign != 0 ||
       (int64_t)splits * span < capacity || (int64_t)(splits - 1) * span >= capacity)
     return QF_E_ARG;

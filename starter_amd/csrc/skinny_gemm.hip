@@ -45,6 +45,7 @@
 // exactly representable f32 (e.g. integer inputs below 2^24), and otherwise
 // differ from it by f32 accumulation error only.
 #include "qf_device.h"
+#include "qf_merge.h"
 #include "qf_silu.h"
 
 namespace qf {
@@ -65,6 +66,11 @@ constexpr int kEpiPartials = 0;  // f32 split-K partials [S, M, N]
 constexpr int kEpiSiluMul = 1;   // packed gate/up -> bf16 silu(gate) * up [M, N]
 constexpr int kEpiArgmax = 2;    // bf16 logits (optional) + argmax candidates per 16-column tile
 
+// Sources of x in skinny_kernel.
+constexpr int kXDirect = 0;  // global loads straight into MFMA layout (up to 4 rows)
+constexpr int kXStaged = 1;  // loaded like W, transposed through the wave's LDS tile
+constexpr int kXMerged = 2;  // merged from attention segments into LDS by a prologue
+
 // Is (v, i) ahead of (bv, bi) in argmax order: larger value, NaN above
 // everything, the lower index on equal values (torch.argmax's first maximum)?
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
@@ -82,6 +88,14 @@ struct SkinnyArgs {
   int32_t m;
   int32_t n;           // output columns
   int32_t chunks;      // 64-wide k chunks per split
+  // kXMerged only: x row m, columns [128 h, 128 h + 128), is the merge of the
+  // attention segments of virtual head m * seg_kv_heads + h / seg_groups,
+  // query group h % seg_groups (partials [V, S, G, 128], stats [V, S, 2, G]).
+  const float* seg_partials;
+  const float* seg_stats;
+  int32_t seg_splits;
+  int32_t seg_groups;
+  int32_t seg_kv_heads;
 };
 
 __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, const f32x4& c) {
@@ -217,13 +231,23 @@ __device__ __forceinline__ void finish(const SkinnyArgs& a, f32x4 (&acc)[NT][MT]
 // MT m-tiles of x (M <= 16*MT); NT n-tiles of W per wave (for PAIRS the
 // first NT/2 are gate tiles, the rest the matching up tiles); the four waves
 // form WN = 4/WK groups of distinct n-tiles, each group WK waves that split
-// the chunks; D chunks in flight per wave; NTL = nontemporal weight loads.
-// Waves of different groups read the same x chunk at about the same time,
-// so x is fetched from L2 once per workgroup rather than once per wave.
-template <int MT, int NT, int WK, int D, int EPI, bool NTL, bool XT>
+// the chunks; D chunks in flight per wave; NTL = nontemporal weight loads;
+// XS = source of x (kXDirect, kXStaged, kXMerged).  Waves of different
+// groups read the same x chunk at about the same time, so x is fetched from
+// L2 once per workgroup rather than once per wave.
+//
+// kXMerged (MT = 1): the workgroup's x slice, M rows x (chunks * 64)
+// columns = whole heads of the attention output, is merged from the
+// attention segments by the workgroup itself into dynamic LDS (row stride
+// chunks * 128 + 16 bytes), one wave per (row, head), after the first D
+// weight chunks are issued, so the merge's loads overlap the weight loads.
+template <int MT, int NT, int WK, int D, int EPI, bool NTL, int XS>
 __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
   constexpr bool PAIRS = EPI == kEpiSiluMul;
+  constexpr bool XT = XS == kXStaged;
+  constexpr bool XM = XS == kXMerged;
   static_assert(kWaves % WK == 0, "wave split");
+  static_assert(!XM || MT == 1, "merged x holds at most 16 rows");
   constexpr int WN = kWaves / WK;
   constexpr int kCols = PAIRS ? NT / 2 : NT;  // output n-tiles per wave
   constexpr int kStageTiles = NT + (XT ? MT : 0);
@@ -231,6 +255,7 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
   constexpr int kHandoffBytes = WN * (WK - 1) * NT * MT * kWave * 16;
   __shared__ __attribute__((aligned(16)))
       uint8_t lds[kStageBytes > kHandoffBytes ? kStageBytes : kHandoffBytes];
+  extern __shared__ __attribute__((aligned(16))) uint8_t xm_lds[];
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -263,7 +288,7 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
       if constexpr (XT) {  // coalesced like W, transposed through LDS
         const int row = kTile * mt + kRowsPerLoad * i + lane / 8;
         xp[mt][i] = a.x + (int64_t)(row < a.m ? row : 0) * a.k + kbase + 8 * (lane % 8);
-      } else {             // straight into MFMA layout
+      } else if constexpr (!XM) {  // straight into MFMA layout
         const int row = kTile * mt + r;
         xp[mt][i] = a.x + (int64_t)(row < a.m ? row : 0) * a.k + kbase + 8 * g + kStep * i;
       }
@@ -271,6 +296,8 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
   uint8_t* stage = lds + wave * kStageTiles * kTileLds;
   const int wr_off = (lane / 8) * kLdsRow + 16 * (lane % 8);
   const int rd_off = r * kLdsRow + 16 * g;
+  const int xm_row = a.chunks * kChunk * 2 + 16;
+  const int xm_off = (r < a.m ? r : 0) * xm_row + 16 * g;
 
   f32x4 acc[NT][MT];
 #pragma unroll
@@ -288,12 +315,49 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int i = 0; i < 2; ++i) wv[d][t][i] = load16<NTL>(wp[t] + off + i * wstep);
+    if constexpr (!XM) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) xv[d][mt][i] = load16<false>(xp[mt][i] + off);
+        for (int i = 0; i < 2; ++i) xv[d][mt][i] = load16<false>(xp[mt][i] + off);
+    }
   };
-  auto consume = [&](int d) {
+  // The merged-x prologue: wave w merges (row, head) pairs w, w + 4, ... of
+  // the split's K range.  The first pair's loads are issued before the
+  // weight loads (merge_first, from the pipeline) and combined after them
+  // (merge_x), so the merge overlaps the weight fetch.  Every thread of the
+  // workgroup takes part.
+  const int heads = XM ? a.chunks * kChunk / 128 : 0;  // heads in this split's K range
+  const int q0 = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform by construction
+  SegmentLoads seg;
+  auto pair = [&](int q, int64_t& vh, int& g, int& off) {
+    const int m = q / heads, hl = q - m * heads, h = (int)(kbase / 128) + hl;
+    vh = (int64_t)m * a.seg_kv_heads + h / a.seg_groups;
+    g = h % a.seg_groups;
+    off = m * xm_row + hl * 256;
+  };
+  auto merge_first = [&]() {
+    if constexpr (XM) {
+      if (q0 < a.m * heads) {
+        int64_t vh; int g, off;
+        pair(q0, vh, g, off);
+        merge_issue(seg, a.seg_partials, a.seg_stats, vh, a.seg_splits, a.seg_groups, g, lane);
+      }
+    }
+  };
+  auto merge_x = [&]() {
+    if constexpr (XM) {
+      for (int q = q0; q < a.m * heads; q += kWaves) {
+        int64_t vh; int g, off;
+        pair(q, vh, g, off);
+        if (q != q0) merge_issue(seg, a.seg_partials, a.seg_stats, vh, a.seg_splits, a.seg_groups, g, lane);
+        reinterpret_cast<uint32_t*>(xm_lds + off)[lane] =
+            merge_finish(seg, a.seg_partials, vh, a.seg_splits, a.seg_groups, g, lane);
+      }
+      __syncthreads();
+    }
+  };
+  auto consume = [&](int d, int j) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -316,9 +380,14 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
       for (int t = 0; t < NT; ++t)
         fw[t][s] = *reinterpret_cast<const uint4*>(stage + t * kTileLds + rd_off + s * kStep * 2);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        fx[mt][s] = XT ? *reinterpret_cast<const uint4*>(stage + (NT + mt) * kTileLds + rd_off + s * kStep * 2)
-                       : xv[d][mt][s];
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (XT)
+          fx[mt][s] = *reinterpret_cast<const uint4*>(stage + (NT + mt) * kTileLds + rd_off + s * kStep * 2);
+        else if constexpr (XM)
+          fx[mt][s] = *reinterpret_cast<const uint4*>(xm_lds + xm_off + (wk + WK * j) * kChunk * 2 + s * kStep * 2);
+        else
+          fx[mt][s] = xv[d][mt][s];
+      }
     }
     wave_lds_fence();
 #pragma unroll
@@ -332,33 +401,36 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
   // Software pipeline with D chunks in flight.  The steady-state loop issues
   // unconditionally, so the compiler's wait counts stay exact (each consume
   // waits only for its own chunk); only the last 2*D chunks take branches.
+  merge_first();
   if (n_own >= D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(d, d);
+    merge_x();
     int j = 0;
     for (; j + 2 * D <= n_own; j += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        consume(d);
+        consume(d, j + d);
         issue(d, j + d + D);
       }
     }
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      consume(d);
+      consume(d, j + d);
       if (j + d + D < n_own) issue(d, j + d + D);
     }
     j += D;
 #pragma unroll
     for (int d = 0; d < D; ++d)
-      if (j + d < n_own) consume(d);
+      if (j + d < n_own) consume(d, j + d);
   } else {
 #pragma unroll
     for (int d = 0; d < D; ++d)
       if (d < n_own) issue(d, d);
+    merge_x();
 #pragma unroll
     for (int d = 0; d < D; ++d)
-      if (d < n_own) consume(d);
+      if (d < n_own) consume(d, d);
   }
 
   finish<MT, NT, WK, EPI>(a, acc, lds, lane, wk, wn, col0, live, split);
@@ -568,12 +640,12 @@ int plan_splits(int64_t rows, int64_t k, int64_t n) {
   return (int)s;
 }
 
-template <int MT, int NT, int WK, int D, int EPI, bool NTL, bool XT>
-int launch(const SkinnyArgs& a, int splits, hipStream_t s) {
+template <int MT, int NT, int WK, int D, int EPI, bool NTL, int XS>
+int launch(const SkinnyArgs& a, int splits, hipStream_t s, size_t dyn_lds = 0) {
   constexpr int kColsPerBlock = kTile * (EPI == kEpiSiluMul ? NT / 2 : NT) * (kWaves / WK);
   const int64_t grid_x = (a.n + kColsPerBlock - 1) / kColsPerBlock;
-  hipLaunchKernelGGL((skinny_kernel<MT, NT, WK, D, EPI, NTL, XT>),
-                     dim3((unsigned)grid_x, (unsigned)splits), dim3(kBlock), 0, s, a);
+  hipLaunchKernelGGL((skinny_kernel<MT, NT, WK, D, EPI, NTL, XS>),
+                     dim3((unsigned)grid_x, (unsigned)splits), dim3(kBlock), dyn_lds, s, a);
   return launch_status();
 }
 
@@ -610,12 +682,12 @@ int dispatch_partials(const SkinnyArgs& a, int splits, hipStream_t s) {
   }
   switch (mt) {
     case 1:
-      if (a.m <= 4) return launch<1, 1, 4, 2, kEpiPartials, true, false>(a, splits, s);
-      if (a.n / kTile >= 256) return launch<1, 2, 4, 2, kEpiPartials, true, true>(a, splits, s);
-      return launch<1, 1, 4, 2, kEpiPartials, true, true>(a, splits, s);
-    case 2: return launch<2, 2, 4, 2, kEpiPartials, true, true>(a, splits, s);
-    case 3: return launch<3, 2, 4, 2, kEpiPartials, true, true>(a, splits, s);
-    default: return launch<4, 2, 4, 2, kEpiPartials, true, true>(a, splits, s);
+      if (a.m <= 4) return launch<1, 1, 4, 2, kEpiPartials, true, kXDirect>(a, splits, s);
+      if (a.n / kTile >= 256) return launch<1, 2, 4, 2, kEpiPartials, true, kXStaged>(a, splits, s);
+      return launch<1, 1, 4, 2, kEpiPartials, true, kXStaged>(a, splits, s);
+    case 2: return launch<2, 2, 4, 2, kEpiPartials, true, kXStaged>(a, splits, s);
+    case 3: return launch<3, 2, 4, 2, kEpiPartials, true, kXStaged>(a, splits, s);
+    default: return launch<4, 2, 4, 2, kEpiPartials, true, kXStaged>(a, splits, s);
   }
 }
 
@@ -624,8 +696,8 @@ int dispatch_partials(const SkinnyArgs& a, int splits, hipStream_t s) {
 int dispatch_silu(const SkinnyArgs& a, hipStream_t s) {
   switch ((a.m + kTile - 1) / kTile) {
     case 1:
-      if (a.m <= 4) return launch<1, 2, 4, 4, kEpiSiluMul, true, false>(a, 1, s);
-      return launch<1, 2, 4, 4, kEpiSiluMul, true, true>(a, 1, s);
+      if (a.m <= 4) return launch<1, 2, 4, 4, kEpiSiluMul, true, kXDirect>(a, 1, s);
+      return launch<1, 2, 4, 4, kEpiSiluMul, true, kXStaged>(a, 1, s);
     case 2: return launch_xs<2, 2, 1, 4, kEpiSiluMul>(a, 1, s);
     case 3: return launch_xs<3, 2, 1, 4, kEpiSiluMul>(a, 1, s);
     default: return launch_xs<4, 2, 1, 4, kEpiSiluMul>(a, 1, s);
@@ -684,10 +756,10 @@ int dispatch_argmax(const SkinnyArgs& a, hipStream_t s) {
   switch ((a.m + kTile - 1) / kTile) {
     case 1:
       if (a.m == 1 || !two) {
-        if (a.m <= 4) return launch<1, 1, 4, 4, kEpiArgmax, true, false>(a, 1, s);
+        if (a.m <= 4) return launch<1, 1, 4, 4, kEpiArgmax, true, kXDirect>(a, 1, s);
         return launch_xs<1, 1, 1, 4, kEpiArgmax>(a, 1, s);
       }
-      if (a.m <= 4) return launch<1, 2, 4, 4, kEpiArgmax, true, false>(a, 1, s);
+      if (a.m <= 4) return launch<1, 2, 4, 4, kEpiArgmax, true, kXDirect>(a, 1, s);
       return launch_xs<1, 2, 2, 4, kEpiArgmax>(a, 1, s);
     case 2: return launch_xs<2, 1, 1, 4, kEpiArgmax>(a, 1, s);
     case 3: return launch_xs<3, 1, 1, 4, kEpiArgmax>(a, 1, s);
@@ -753,6 +825,46 @@ extern "C" int qf_linear_partials(const void* x, int64_t rows, int64_t k, const 
   a.n = (int32_t)n;
   a.chunks = (int32_t)(k / kChunk / splits);
   return dispatch_partials(a, splits, as_stream(stream));
+}
+
+extern "C" int qf_linear_partials_merged(const float* seg_partials, const float* seg_stats,
+                                         int32_t seg_splits, int64_t batch, int32_t q_heads,
+                                         int32_t kv_heads, const void* weight, int64_t n,
+                                         int32_t splits, void* partials, void* stream) {
+  if (batch < 1 || batch > kTile || q_heads < 1 || kv_heads < 1 || q_heads % kv_heads != 0 ||
+      q_heads / kv_heads > 16)
+    return QF_E_SHAPE;
+  const int64_t k = (int64_t)q_heads * 128;
+  const int st = shape_status(batch, k, n);
+  if (st != QF_OK) return st;
+  if (!seg_partials || !seg_stats || !weight || !partials) return QF_E_ARG;
+  if (seg_splits < 2 || seg_splits > kMaxSegments) return QF_E_ARG;
+  if (splits < 1 || (k / kChunk) % splits != 0 || (k / kChunk / splits) % 2 != 0) return QF_E_ARG;
+  const int64_t chunks = k / kChunk / splits;
+  const size_t lds = (size_t)batch * (size_t)(chunks * kChunk * 2 + 16);
+  if (lds > (64u << 10)) return QF_E_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(seg_partials) & 7u) != 0 ||
+      (reinterpret_cast<uintptr_t>(seg_stats) & 3u) != 0 || !aligned16(weight) ||
+      !aligned16(partials))
+    return QF_E_ALIGN;
+  SkinnyArgs a;
+  a.x = nullptr;
+  a.w = static_cast<const uint16_t*>(weight);
+  a.partials = static_cast<float*>(partials);
+  a.out = nullptr;
+  a.k = k;
+  a.m = (int32_t)batch;
+  a.n = (int32_t)n;
+  a.chunks = (int32_t)chunks;
+  a.seg_partials = seg_partials;
+  a.seg_stats = seg_stats;
+  a.seg_splits = seg_splits;
+  a.seg_groups = q_heads / kv_heads;
+  a.seg_kv_heads = kv_heads;
+  // The same tile plan (and so the same f32 addition order) as
+  // qf_linear_partials for up to 16 rows: one 16-row x tile, four waves
+  // splitting each workgroup's chunks, two chunks in flight.
+  return launch<1, 1, 4, 2, kEpiPartials, true, kXMerged>(a, splits, as_stream(stream), lds);
 }
 
 extern "C" int qf_linear_silu_mul(const void* x, int64_t rows, int64_t k, const void* gate_up,

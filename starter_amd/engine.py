@@ -13,7 +13,8 @@ reference runs:
 * decode (``engine/decode_step.py:33-64``): the split-K projections whose f32
   partials feed ``add_rms_norm`` and the split-KV decode attention (which
   also does ``qkv_norm_rope_cache``'s Q/K norm, RoPE and cache write in its
-  own launches), the fused gate/up projection with its SiLU epilogue, and
+  own launches; at small batches the o_proj projection merges the attention's
+  key segments itself), the fused gate/up projection with its SiLU epilogue, and
   the LM head fused with the greedy token choice; the whole step is captured once per
   (batch, capacity) in a HIP graph and replayed with the position and cache
   lengths advanced on the device.
@@ -38,7 +39,8 @@ from .kernels import lm_head as _lm_head
 from .kernels.prefill import prefill_qkv
 from .kernels.rmsnorm import rms_norm
 from .kernels.rotary import rope_tables
-from .kernels.skinny_gemm import linear_partials, linear_silu_mul, supports
+from .kernels.skinny_gemm import (linear_partials, linear_partials_merged, linear_silu_mul,
+                                  supports, supports_merged)
 from .kernels.small_query_attention import SmallQueryAttention
 
 HEAD = 128
@@ -80,6 +82,10 @@ def pack_layer(layer) -> PackedLayer:
     )
 
 
+#: Largest batch whose decode step merges attention segments inside o_proj.
+MERGED_O_BATCH = 1
+
+
 class _State:
     """Caches, rotary tables and graph buffers for one (batch, capacity)."""
 
@@ -91,6 +97,11 @@ class _State:
         self.values = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in engine.layers]
         self.cos, self.sin = rope_tables(engine.inv_freq, capacity, device=dev)
         self.attention = SmallQueryAttention(batch, engine.q_heads, engine.kv_heads, capacity, dev)
+        # o_proj merges the attention's key segments itself (one launch fewer
+        # per layer) up to MERGED_O_BATCH sequences.
+        self.merged_o = (batch <= MERGED_O_BATCH and self.attention.splits > 1
+                         and supports_merged(self.attention.partials, self.attention.stats, batch,
+                                             engine.layers[0].o))
         self.tokens = torch.zeros(batch, dtype=torch.int64, device=dev)
         self.position = torch.zeros(1, dtype=torch.int64, device=dev)
         self.used = torch.zeros(batch * engine.kv_heads, dtype=torch.int32, device=dev)
@@ -211,12 +222,15 @@ class Engine:
         normed = rms_norm(x, first.ln_in, first.eps_in)
         for index, layer in enumerate(self.layers):
             # qkv_norm_rope_cache + attention, fused into the attention launches
-            attended = st.attention.run_qkv(self._project(normed, layer.qkv), layer.q_norm,
-                                            layer.k_norm, layer.eps_q, layer.eps_k, st.cos, st.sin,
-                                            st.position, st.keys[index], st.values[index],
-                                            st.used, self.scale)
-            x, normed = add_rms_norm(x, self._project(attended.view(batch, -1), layer.o),
-                                     layer.ln_post, layer.eps_post)
+            args = (self._project(normed, layer.qkv), layer.q_norm, layer.k_norm, layer.eps_q,
+                    layer.eps_k, st.cos, st.sin, st.position, st.keys[index], st.values[index],
+                    st.used, self.scale)
+            if st.merged_o:
+                st.attention.run_qkv_unmerged(*args)
+                o = linear_partials_merged(st.attention.partials, st.attention.stats, batch, layer.o)
+            else:
+                o = self._project(st.attention.run_qkv(*args).view(batch, -1), layer.o)
+            x, normed = add_rms_norm(x, o, layer.ln_post, layer.eps_post)
             hidden = self._mlp_hidden(normed, layer.gate_up)
             weight, eps = self._next_norm(index)
             x, normed = add_rms_norm(x, self._project(hidden, layer.down), weight, eps)

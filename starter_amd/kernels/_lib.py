@@ -41,6 +41,8 @@ SIGNATURES = {
     "qf_rope_table": ([_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp], _i32),
     "qf_linear_splits": ([_i64, _i64, _i64], _i32),
     "qf_linear_partials": ([_vp, _i64, _i64, _vp, _i64, _i32, _vp, _vp], _i32),
+    "qf_linear_partials_merged": ([_vp, _vp, _i32, _i64, _i32, _i32, _vp, _i64, _i32, _vp, _vp],
+                                  _i32),
     "qf_linear_silu_mul": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp], _i32),
     "qf_attention_partition": ([_i64, _i64, _i32, _vp, _vp], _i32),
     "qf_decode_attention": ([_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _f32, _i32, _i64, _vp, _vp,

@@ -9,6 +9,9 @@ third argument because the split plan here depends on it.
 * ``linear_partials(x, weight)``: FP32 split-K partial sums ``[S, M, N]`` of
   ``x @ weight.T``.  ``add_rms_norm`` and ``qkv_norm_rope_cache`` add the S
   partials in order and round once to BF16.
+* ``linear_partials_merged(partials, stats, batch, weight)``: the same partials
+  for x = the decode attention's output, merged from its unmerged key
+  segments inside the projection (no merge launch, x never in memory).
 * ``linear_silu_mul(x, gate_up_weight)``: ``bf16(silu(bf16(gate)) * bf16(up))``
   for a packed ``[2N, K]`` weight, with both projections and the SiLU epilogue
   in one launch.
@@ -82,6 +85,59 @@ def linear_partials(x, weight):
     _lib.call("qf_linear_partials", x.data_ptr(), m, k, weight.data_ptr(), n, splits,
               partials.data_ptr(), _lib.stream(x.device))
     return partials
+
+
+#: Most rows (sequences) ``linear_partials_merged`` takes.
+MERGED_MAX_ROWS = 16
+
+
+def _merged_dims(partials, stats, batch, weight):
+    """(segments, q_heads, kv_heads, n, k, splits) or None when the merged
+    projection does not apply to these operands."""
+    if (partials.ndim != 4 or stats.ndim != 4 or weight.ndim != 2 or not 1 <= batch <= MERGED_MAX_ROWS
+            or partials.dtype != torch.float32 or stats.dtype != torch.float32
+            or weight.dtype != torch.bfloat16 or not weight.is_cuda
+            or partials.device != weight.device or stats.device != weight.device
+            or not (partials.is_contiguous() and stats.is_contiguous() and weight.is_contiguous())):
+        return None
+    vheads, segments, groups, width = partials.shape
+    if (width != 128 or tuple(stats.shape) != (vheads, segments, 2, groups) or vheads % batch
+            or not 2 <= segments <= 32 or not 1 <= groups <= 16):
+        return None
+    kv_heads = vheads // batch
+    q_heads = kv_heads * groups
+    n, k = weight.shape
+    if k != q_heads * 128 or n % BN or not _aligned(weight):
+        return None
+    splits = split_count(n, k, batch)
+    chunks = k // BK // splits
+    if chunks % 2 or batch * (chunks * BK * 2 + 16) > 64 * 1024:
+        return None
+    return segments, q_heads, kv_heads, n, k, splits
+
+
+def supports_merged(partials, stats, batch, weight):
+    """Whether ``linear_partials_merged`` takes these operands (a static rule)."""
+    return _merged_dims(partials, stats, batch, weight) is not None
+
+
+def linear_partials_merged(partials, stats, batch, weight):
+    """FP32 split-K partials [S, batch, N] of ``attended @ weight.T``, where
+    ``attended`` [batch, Hq * 128] is the merge of the attention's unmerged
+    key segments (``partials`` [B*Hkv, segments, G, 128] and ``stats``
+    [B*Hkv, segments, 2, G], as ``SmallQueryAttention.run_qkv_unmerged``
+    leaves them).  Bit-identical to ``linear_partials`` of the merged
+    attention output; replaces the hand-off engine/decode_step.py:48-52."""
+    dims = _merged_dims(partials, stats, batch, weight)
+    if dims is None:
+        raise ValueError("expected contiguous FP32 attention segments [V, S, G, 128] / [V, S, 2, G] "
+                         "and a BF16 CUDA weight [N, Hq*128] the merged plan covers")
+    segments, q_heads, kv_heads, n, k, splits = dims
+    out = torch.empty((splits, batch, n), dtype=torch.float32, device=weight.device)
+    _lib.call("qf_linear_partials_merged", partials.data_ptr(), stats.data_ptr(), segments, batch,
+              q_heads, kv_heads, weight.data_ptr(), n, splits, out.data_ptr(),
+              _lib.stream(weight.device))
+    return out
 
 
 def linear_silu_mul(x, gate_up_weight):

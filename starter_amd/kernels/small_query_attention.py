@@ -92,6 +92,23 @@ class SmallQueryAttention:
         same arguments and the same results bit for bit (the new K/V row lands
         in slot ``position`` of the caches, Q never goes to memory).  ``qkv``
         is BF16 [B, (Hq + 2 Hkv) * 128] or FP32 split-K partials [S, B, ...]."""
+        return self._qkv(qkv, q_weight, k_weight, q_eps, k_eps, cos, sin, position, key_cache,
+                         value_cache, used, scale, merge=True)
+
+    def run_qkv_unmerged(self, qkv, q_weight, k_weight, q_eps, k_eps, cos, sin, position,
+                         key_cache, value_cache, used, scale):
+        """``run_qkv`` without the segment merge: the per-segment partials and
+        statistics stay in ``self.partials`` / ``self.stats`` (valid until the
+        next call on this instance) for ``skinny_gemm.linear_partials_merged``,
+        which merges them inside the o_proj projection.  Needs ``splits > 1``;
+        returns None."""
+        if self.splits < 2:
+            raise ValueError("unmerged attention needs more than one key segment")
+        self._qkv(qkv, q_weight, k_weight, q_eps, k_eps, cos, sin, position, key_cache,
+                  value_cache, used, scale, merge=False)
+
+    def _qkv(self, qkv, q_weight, k_weight, q_eps, k_eps, cos, sin, position, key_cache,
+             value_cache, used, scale, merge):
         device = self.partials.device
         width = (self.hq + 2 * self.hk) * HEAD
         if qkv.dtype == torch.float32 and qkv.ndim == 3:
@@ -115,11 +132,12 @@ class SmallQueryAttention:
                        for t in bf16)):
             raise ValueError("expected packed BF16 Q/K/V (or FP32 partials), BF16 gains, rotary "
                              "tables and caches, an int64 position and int32 lengths on one device")
-        out = torch.empty((self.batch, 1, self.hq, HEAD), dtype=torch.bfloat16, device=device)
+        out = (torch.empty((self.batch, 1, self.hq, HEAD), dtype=torch.bfloat16, device=device)
+               if merge else None)
         _lib.call("qf_decode_attention_qkv", qkv.data_ptr(), qkv_splits, q_weight.data_ptr(),
                   k_weight.data_ptr(), float(q_eps), float(k_eps), cos.data_ptr(), sin.data_ptr(),
                   position.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
                   used.data_ptr(), self.batch, self.hq, self.hk, self.capacity, float(scale),
                   self.splits, self.span, self.partials.data_ptr(), self.stats.data_ptr(),
-                  out.data_ptr(), _lib.stream(device))
+                  out.data_ptr() if merge else None, _lib.stream(device))
         return out

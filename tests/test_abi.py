@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 18
+    assert len(names) == 19
 
 
 def test_library_exports_every_symbol():
@@ -79,6 +79,19 @@ def test_host_side_argument_errors_launch_nothing():
     assert lib.qf_linear_partials(bogus + 8, 4, 2560, bogus, 6144, 1, bogus, None) == -3
     assert lib.qf_linear_partials(bogus, 65, 2560, bogus, 6144, 1, bogus, None) == -2
     assert lib.qf_linear_silu_mul(bogus, 4, 2560, bogus, 9728, bogus + 4, None) == -3
+    # projection of the unmerged attention segments: rows, heads, segments, splits, LDS, alignment
+    merged = lib.qf_linear_partials_merged
+    assert merged(bogus, bogus, 9, 17, 32, 8, bogus, 2560, 8, bogus, None) == -2
+    assert merged(bogus, bogus, 9, 1, 32, 6, bogus, 2560, 8, bogus, None) == -2
+    assert merged(bogus, bogus, 9, 1, 32, 8, bogus, 2570, 8, bogus, None) == -2
+    assert merged(bogus, bogus, 1, 1, 32, 8, bogus, 2560, 8, bogus, None) == -1  # one segment
+    assert merged(bogus, bogus, 33, 1, 32, 8, bogus, 2560, 8, bogus, None) == -1
+    assert merged(bogus, bogus, 9, 1, 32, 8, bogus, 2560, 3, bogus, None) == -1
+    assert merged(bogus, bogus, 9, 1, 32, 8, bogus, 2560, 64, bogus, None) == -1  # half heads
+    assert merged(None, bogus, 9, 1, 32, 8, bogus, 2560, 8, bogus, None) == -1
+    assert merged(bogus, bogus, 9, 16, 32, 8, bogus, 2560, 1, bogus, None) == -2  # > 64 KiB LDS
+    assert merged(bogus + 4, bogus, 9, 1, 32, 8, bogus, 2560, 8, bogus, None) == -3
+    assert merged(bogus, bogus, 9, 1, 32, 8, bogus, 2560, 8, bogus + 8, None) == -3
     assert lib.qf_linear_silu_mul(bogus, 4, 2560, bogus, 9720, bogus, None) == -2
     # LM head: shape rule and alignment
     assert lib.qf_lm_head_blocks(151936) == 9496 and lib.qf_lm_head_blocks(100) == -2
@@ -102,6 +115,8 @@ def test_host_side_argument_errors_launch_nothing():
                                    None, None, bogus, None) == -1
     assert lib.qf_decode_attention(bogus + 2, bogus, bogus, bogus, 1, 8, 2, 64, 0.1, 1, 64, None,
                                    None, bogus, None) == -3
+    assert lib.qf_decode_attention(bogus, bogus, bogus, bogus, 1, 8, 2, 64, 0.1, 1, 64, None,
+                                   None, None, None) == -1            # one segment needs out
     # fused Q/K/V + attention: the attention rules, then the Q/K/V operands
     fused = lib.qf_decode_attention_qkv
     assert fused(bogus, 0, bogus, bogus, 1e-6, 1e-6, bogus, bogus, bogus, bogus, bogus, bogus,

@@ -45,7 +45,7 @@ def engine():
     return Engine(config=Qwen3Config(**TINY), seed=3)
 
 
-@pytest.mark.parametrize("batch,length,steps", [(1, 5, 6), (3, 37, 5), (4, 64, 4)])
+@pytest.mark.parametrize("batch,length,steps", [(1, 5, 6), (1, 70, 4), (3, 37, 5), (4, 64, 4)])
 def test_generation_matches_native_teacher_forced(engine, batch, length, steps):
     g = torch.Generator().manual_seed(batch * 100 + length)
     prompts = torch.randint(0, TINY["vocab_size"], (batch, length), generator=g).tolist()
@@ -63,6 +63,8 @@ def test_generation_matches_native_teacher_forced(engine, batch, length, steps):
     clear = (top2[..., 0] - top2[..., 1]) > 0.25
     assert torch.equal(tokens[clear], expected.argmax(-1)[clear])
     assert bool(clear.any())
+    if (batch, length) == (1, 70):  # two key segments: o_proj merges them itself
+        assert engine._states[(1, length + steps)].merged_o
 
 
 def test_graph_replay_equals_eager(engine):

@@ -356,6 +356,32 @@ def test_skinny_marshalling():
     assert (name, m, k, n) == ("qf_linear_silu_mul", 5, 2560, 9728)
 
 
+def test_skinny_merged_rule_and_marshalling():
+    """o_proj over unmerged attention segments: Qwen3-4B's 32/8 heads at batch 1."""
+    from starter_amd.kernels import skinny_gemm as sk
+    f32 = torch.float32
+    parts, stats, w = Fake((8, 9, 4, 128), f32), Fake((8, 9, 2, 4), f32), Fake((2560, 4096))
+    assert sk.supports_merged(parts, stats, 1, w)
+    with recorded() as calls:
+        out = sk.linear_partials_merged(parts, stats, 1, w)
+    splits = sk.split_count(2560, 4096, 1)
+    assert tuple(out.shape) == (splits, 1, 2560) and out.dtype == f32
+    name, pp, ps, segs, batch, hq, hk, pw, n, s, po = calls[0][:11]
+    assert (name, segs, batch, hq, hk, n, s) == ("qf_linear_partials_merged", 9, 1, 32, 8, 2560, splits)
+    assert (pp, ps, pw, po) == (parts.data_ptr(), stats.data_ptr(), w.data_ptr(), out.data_ptr())
+    # batch 2 of the same heads: 16 virtual heads
+    assert sk.supports_merged(Fake((16, 9, 4, 128), f32), Fake((16, 9, 2, 4), f32), 2, w)
+    for bad in ((Fake((8, 1, 4, 128), f32), Fake((8, 1, 2, 4), f32), 1, w),     # one segment
+                (parts, Fake((8, 9, 2, 2), f32), 1, w),                          # stats mismatch
+                (parts, stats, 1, Fake((2560, 2048))),                           # k != Hq * 128
+                (parts, stats, 3, w),                                            # 8 % 3
+                (Fake((8, 9, 4, 128), BF16), stats, 1, w),
+                (parts, stats, 1, Fake((2560, 4096), cuda=False))):
+        assert not sk.supports_merged(*bad)
+        with pytest.raises(ValueError):
+            sk.linear_partials_merged(*bad)
+
+
 def test_attention_partition_contract():
     """The reference test's grid (tests/test_small_query_attention.py:217-230)."""
     from starter_amd.kernels.small_query_attention import partition_keys
@@ -423,6 +449,18 @@ def test_attention_context_validation_and_marshalling():
                        (11, float("inf"))):
         with pytest.raises(ValueError), torch.no_grad():
             plan.run_qkv(*good[:index], bad, *good[index + 1:])
+    # unmerged: same launch with no output (the segments stay in the scratch)
+    with recorded() as calls, torch.no_grad():
+        plan.run_qkv(*good)
+        assert plan.run_qkv_unmerged(*good) is None
+    assert calls[1][0] == "qf_decode_attention_qkv" and calls[1][-2] is None
+    assert calls[1][:-2] == calls[0][:-2] and plan.splits > 1
+    with mock.patch.object(torch.cuda, "get_device_properties", return_value=props), \
+            mock.patch.object(torch, "empty", side_effect=fake):
+        single = sqa.SmallQueryAttention(2, 8, 2, 64, "cuda:0")
+    assert single.splits == 1
+    with pytest.raises(ValueError), torch.no_grad():
+        single.run_qkv_unmerged(*good)
 
 
 def test_lm_head_rule_and_marshalling():
