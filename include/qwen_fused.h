@@ -223,7 +223,7 @@ int qf_linear_silu_mul(const void* x, int64_t rows, int64_t k, const void* gate_
 /*
  * Key-segment plan of qf_decode_attention for virtual_heads = batch * Hkv
  * heads of a cache with `capacity` slots on a GPU with compute_units CUs:
- * about 1.25 workgroups per CU, segments of whole 64-key tiles, at most 32.
+ * at most one workgroup per CU, segments of whole 64-key tiles, at most 32.
  * Writes *splits >= 1 and *span (keys per segment, a multiple of 64) with
  * (splits - 1) * span < capacity <= splits * span.
  * Replaces partition_keys (engine/kernels/small_query_attention.py:24-38).

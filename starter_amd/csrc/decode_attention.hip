@@ -715,13 +715,14 @@ using namespace qf;
 extern "C" int qf_attention_partition(int64_t virtual_heads, int64_t capacity,
                                       int32_t compute_units, int32_t* splits, int64_t* span) {
   if (virtual_heads < 1 || capacity < 1 || compute_units < 1 || !splits || !span) return QF_E_ARG;
-  // About 1.25 workgroups per compute unit (measured at batch x keys =
-  // 1 x 545, 4 x 2081, 16 x 641 against every split count: fewer segments
-  // lengthen each workgroup's chain, more cost merge work and doubly loaded
-  // CUs), at least one 64-key tile per segment, at most 32 segments;
-  // segments are whole 64-key tiles.
+  // At most one workgroup per compute unit (measured with the matrix-core
+  // kernel at batch x keys from 1 x 545 to 64 x 1024 against every split
+  // count: a CU that runs two segments finishes last, so 1.25 per CU - the
+  // earlier plan - cost 4-17% at batch 4 x 545, 16 and 32; fewer segments
+  // lengthen each workgroup's chain), at least one 64-key tile per segment,
+  // at most 32 segments; segments are whole 64-key tiles.
   const int64_t tiles = (capacity + 63) / 64;
-  const int64_t desired = (5 * (int64_t)compute_units + 4 * virtual_heads - 1) / (4 * virtual_heads);
+  const int64_t desired = (int64_t)compute_units / virtual_heads;
   int64_t s = desired < 1 ? 1 : desired;
   if (s > tiles) s = tiles;
   if (s > kMaxSplits) s = kMaxSplits;

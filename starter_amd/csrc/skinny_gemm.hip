@@ -18,9 +18,8 @@
 // touch 16 different rows; HBM streams far better when each row is read a
 // whole 128-byte line at a time.  So W moves in 64-wide k chunks: one
 // 16-byte load per lane reads 8 rows x 128 contiguous bytes (two loads per
-// 16-row tile), the wave writes the chunk to its own LDS staging tile (row
-// stride padded to 144 bytes, conflict-free both ways) and reads it back in
-// MFMA layout.  Only the wave itself touches its staging tile, so no
+// 16-row tile), the wave writes the chunk to its own LDS staging tile
+// (XOR-swizzled, conflict-free both ways) and reads it back in MFMA layout.  Only the wave itself touches its staging tile, so no
 // workgroup barrier is needed in the loop.  Each wave keeps D chunks of loads
 // in flight (software pipelined).
 //
@@ -112,8 +111,16 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-constexpr int kLdsRow = kChunk * 2 + 16;       // padded staging row: 144 bytes
+// Staging tiles: 128-byte rows, 16-byte piece c of row r stored at piece
+// c ^ ((r >> 1) & 7).  Both access patterns then touch 16 distinct 16-byte
+// bank groups per 16 lanes: the chunk loads' writes (rows r, r + 1, all
+// eight pieces) and the MFMA-layout reads (rows 0..15, one piece).  Same
+// bits as padded 144-byte rows, 2-3% faster at 64 rows.
+constexpr int kLdsRow = kChunk * 2;            // staging row bytes
 constexpr int kTileLds = kTile * kLdsRow;      // one 16-row staging tile
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+  return row * kLdsRow + 16 * (chunk ^ ((row >> 1) & 7));
+}
 constexpr int kRowsPerLoad = kWave * 16 / (kChunk * 2);  // 8 rows x 128 B per load
 
 // Wave hand-off and epilogue shared by the kernel variants: waves wk > 0 of
@@ -319,8 +326,8 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
       }
     }
   uint8_t* stage = lds + wave * kStageTiles * kTileLds;
-  const int wr_off = (lane / 8) * kLdsRow + 16 * (lane % 8);
-  const int rd_off = r * kLdsRow + 16 * g;
+  const int wr_off[2] = {lds_off(lane / 8, lane % 8), lds_off(lane / 8 + kRowsPerLoad, lane % 8)};
+  const int rd_off[2] = {lds_off(r, g), lds_off(r, g + 4)};
   const int xm_row = a.chunks * kChunk * 2 + 16;
   const int xm_off = (r < a.m ? r : 0) * xm_row + 16 * g;
 
@@ -387,14 +394,14 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        *reinterpret_cast<uint4*>(stage + t * kTileLds + wr_off + i * kRowsPerLoad * kLdsRow) =
+        *reinterpret_cast<uint4*>(stage + t * kTileLds + wr_off[i]) =
             wv[d][t][i];
     if constexpr (XT) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-          *reinterpret_cast<uint4*>(stage + (NT + mt) * kTileLds + wr_off + i * kRowsPerLoad * kLdsRow) =
+          *reinterpret_cast<uint4*>(stage + (NT + mt) * kTileLds + wr_off[i]) =
               xv[d][mt][i];
     }
     wave_lds_fence();
@@ -403,11 +410,11 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        fw[t][s] = *reinterpret_cast<const uint4*>(stage + t * kTileLds + rd_off + s * kStep * 2);
+        fw[t][s] = *reinterpret_cast<const uint4*>(stage + t * kTileLds + rd_off[s]);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         if constexpr (XT)
-          fx[mt][s] = *reinterpret_cast<const uint4*>(stage + (NT + mt) * kTileLds + rd_off + s * kStep * 2);
+          fx[mt][s] = *reinterpret_cast<const uint4*>(stage + (NT + mt) * kTileLds + rd_off[s]);
         else if constexpr (XM)
           fx[mt][s] = *reinterpret_cast<const uint4*>(xm_lds + xm_off + (wk + WK * j) * kChunk * 2 + s * kStep * 2);
         else
@@ -524,13 +531,13 @@ __global__ __launch_bounds__(kBlock) void skinny_xs_kernel(SkinnyArgs a) {
     const int wkp = pc / (8 * kRows);
     const int row = (pc / 8) % kRows;
     xp[i] = a.x + (int64_t)(row < a.m ? row : 0) * a.k + kbase + (int64_t)wkp * kChunk + 8 * (pc % 8);
-    xoff[i] = (wkp * kRows + row) * kLdsRow + 16 * (pc % 8);
+    xoff[i] = lds_off(wkp * kRows + row, pc % 8);
   }
   uint8_t* xring = lds;
   uint8_t* stage = lds + 2 * kXStep + wave * NT * kTileLds;
-  const int wr_off = (lane / 8) * kLdsRow + 16 * (lane % 8);
-  const int rd_off = r * kLdsRow + 16 * g;
-  const int xrd_off = wk * kRows * kLdsRow + rd_off;
+  const int wr_off[2] = {lds_off(lane / 8, lane % 8), lds_off(lane / 8 + kRowsPerLoad, lane % 8)};
+  const int rd_off[2] = {lds_off(r, g), lds_off(r, g + 4)};
+  const int xrd_base = wk * kRows * kLdsRow;  // rows of a multiple of 16 keep the swizzle
 
   f32x4 acc[NT][MT];
 #pragma unroll
@@ -560,7 +567,7 @@ __global__ __launch_bounds__(kBlock) void skinny_xs_kernel(SkinnyArgs a) {
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        *reinterpret_cast<uint4*>(stage + t * kTileLds + wr_off + i * kRowsPerLoad * kLdsRow) =
+        *reinterpret_cast<uint4*>(stage + t * kTileLds + wr_off[i]) =
             wv[d][t][i];
     __syncthreads();
     uint4 fw[NT][2], fx[MT][2];
@@ -568,10 +575,10 @@ __global__ __launch_bounds__(kBlock) void skinny_xs_kernel(SkinnyArgs a) {
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        fw[t][s] = *reinterpret_cast<const uint4*>(stage + t * kTileLds + rd_off + s * kStep * 2);
+        fw[t][s] = *reinterpret_cast<const uint4*>(stage + t * kTileLds + rd_off[s]);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        fx[mt][s] = *reinterpret_cast<const uint4*>(xb + xrd_off + mt * kTileLds + s * kStep * 2);
+        fx[mt][s] = *reinterpret_cast<const uint4*>(xb + xrd_base + mt * kTileLds + rd_off[s]);
     }
     wave_lds_fence();
 #pragma unroll

@@ -32,7 +32,7 @@ HEAD = 128
 
 def partition_keys(virtual_heads, capacity, multiprocessors):
     """(splits, span): key segments of whole KEY_TILE tiles covering capacity,
-    about 1.25 workgroups per compute unit, at most MAX_SPLITS.  Metadata only;
+    at most one workgroup per compute unit, at most MAX_SPLITS.  Metadata only;
     the valid length is read on the device.  Same contract as
     engine/kernels/small_query_attention.py:24-38."""
     if min(virtual_heads, capacity, multiprocessors) < 1:
