@@ -786,11 +786,14 @@ __global__ __launch_bounds__(kBlock) void argmax_finalize_kernel(const uint2* ca
   }
 }
 
-// LM head plans (measured on the Qwen3-4B head, 151936 x 2560, at 1, 4, 8 and
-// 16 rows): up to 4 rows x straight into MFMA layout with four chunks in
-// flight (two n-tiles per wave from 2 rows); 5..16 rows the shared-x kernel
-// with two n-tiles per wave and wave pairs splitting K (20% faster at 16
-// rows than per-wave x staging).  Two-tile plans need vocab % 32 == 0.
+// LM head plans (measured on the Qwen3-4B head, 151936 x 2560, at 1, 4, 8,
+// 16, 32 and 64 rows): up to 4 rows x straight into MFMA layout with four
+// chunks in flight (two n-tiles per wave from 2 rows); 5..16 rows the
+// shared-x kernel with two n-tiles per wave and wave pairs splitting K (20%
+// faster at 16 rows than per-wave x staging); beyond 16 rows two n-tiles
+// per wave, each wave all of K (10% faster at 32 rows and 18% at 64 than one
+// tile: every workgroup re-reads x, so wider workgroups halve that traffic).
+// Two-tile plans need vocab % 32 == 0.
 int dispatch_argmax(const SkinnyArgs& a, hipStream_t s) {
   const bool two = a.n % (2 * kTile) == 0;
   switch ((a.m + kTile - 1) / kTile) {
@@ -801,9 +804,9 @@ int dispatch_argmax(const SkinnyArgs& a, hipStream_t s) {
       }
       if (a.m <= 4) return launch<1, 2, 4, 4, kEpiArgmax, true, kXDirect>(a, 1, s);
       return launch_xs<1, 2, 2, 4, kEpiArgmax>(a, 1, s);
-    case 2: return launch_xs<2, 1, 1, 4, kEpiArgmax>(a, 1, s);
-    case 3: return launch_xs<3, 1, 1, 4, kEpiArgmax>(a, 1, s);
-    default: return launch_xs<4, 1, 1, 4, kEpiArgmax>(a, 1, s);
+    case 2: return two ? launch_xs<2, 2, 1, 4, kEpiArgmax>(a, 1, s) : launch_xs<2, 1, 1, 4, kEpiArgmax>(a, 1, s);
+    case 3: return two ? launch_xs<3, 2, 1, 4, kEpiArgmax>(a, 1, s) : launch_xs<3, 1, 1, 4, kEpiArgmax>(a, 1, s);
+    default: return two ? launch_xs<4, 2, 1, 4, kEpiArgmax>(a, 1, s) : launch_xs<4, 1, 1, 4, kEpiArgmax>(a, 1, s);
   }
 }
 
