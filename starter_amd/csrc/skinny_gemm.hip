@@ -632,17 +632,19 @@ int shape_status(int64_t rows, int64_t k, int64_t n) {
 }
 
 // Shared-x wave layout for 17..64 rows (measured on the Qwen3-4B shapes at
-// M = 32, 48, 64): wide outputs take one n-tile per wave and four waves per
-// chunk step; narrower ones two n-tiles per wave and two chunks per step
-// (one per wave pair) when K is short, else one tile per wave with a deeper
-// pipeline.  D = steps in flight per wave.
+// M = 32 and 64 over tile widths 1-4, wave splits and split counts): each
+// wave all of its workgroup's K range (WK = 1), four steps in flight, and two
+// n-tiles per wave (128 columns per workgroup, half the x re-reads of one)
+// while the grid stays within one workgroup per CU, else one tile.  A CU
+// keeps a bounded number of L1 misses in flight, so the stream needs the
+// workgroups spread over all CUs more than it needs the fewest x re-reads.
+constexpr int64_t kPlanCUs = 256;  // MI355X compute units
 struct XsPlan {
   int nt, wk, d;
 };
-XsPlan xs_plan(int64_t rows, int64_t k, int64_t n) {
-  if (n >= 4096) return {1, 1, rows <= 32 ? 4 : 6};
-  if (k <= 4096) return {2, 2, 4};
-  return {1, 1, 6};
+XsPlan xs_plan(int64_t n, int64_t splits) {
+  const int64_t wide = (n + 8 * kTile - 1) / (8 * kTile) * splits;
+  return wide <= kPlanCUs ? XsPlan{2, 1, 4} : XsPlan{1, 1, 4};
 }
 
 // Power-of-two K splits (measured on the Qwen3-4B projection shapes).  Up to
@@ -650,20 +652,16 @@ XsPlan xs_plan(int64_t rows, int64_t k, int64_t n) {
 // 3072 workgroups of 16 columns (~12 per CU), and the partials (written here,
 // read by the consumer) small: splits * min(M, 16) <= K / 32, at most 8 (o_proj
 // takes the same time at 8 and 16 splits, and its consumer, one workgroup per
-// row, reads half the bytes).  Beyond 16 rows
-// (shared-x kernel): the fewest that give ~150 workgroups, within the same
-// partials bound and whole steps per split.
+// row, reads half the bytes).  Beyond 16 rows (shared-x kernel): K ranges
+// of at most 512 (eight chunks) per workgroup, the fewest splits that give
+// them (Qwen3-4B: qkv 5, o_proj 8, down 19 splits; 10-17% faster at 32 and
+// 64 rows than ~150 workgroups of longer ranges, consumers included).
 int plan_splits(int64_t rows, int64_t k, int64_t n) {
   const int64_t chunks = k / kChunk;
   const int64_t mrows = rows < kTile ? rows : kTile;
   int64_t s = 1;
   if (rows > kTile) {
-    const XsPlan p = xs_plan(rows, k, n);
-    const int64_t cols = kTile * p.nt * (kWaves / p.wk);
-    const int64_t groups = (n + cols - 1) / cols;
-    while (groups * s < 150 && chunks % (2 * s) == 0 && (chunks / (2 * s)) % p.wk == 0 &&
-           2 * s * mrows <= k / 32)
-      s *= 2;
+    while (chunks / s > 8 || chunks % s != 0) ++s;
     return (int)s;
   }
   const int64_t tiles = n / kTile;
@@ -695,9 +693,8 @@ int launch_xs(const SkinnyArgs& a, int splits, hipStream_t s) {
 
 template <int MT>
 int dispatch_xs_partials(const SkinnyArgs& a, const XsPlan& p, int splits, hipStream_t s) {
-  if (p.wk == 2) return launch_xs<MT, 2, 2, 4, kEpiPartials>(a, splits, s);
-  if (p.d == 4) return launch_xs<MT, 1, 1, 4, kEpiPartials>(a, splits, s);
-  return launch_xs<MT, 1, 1, 6, kEpiPartials>(a, splits, s);
+  if (p.nt == 2) return launch_xs<MT, 2, 1, 4, kEpiPartials>(a, splits, s);
+  return launch_xs<MT, 1, 1, 4, kEpiPartials>(a, splits, s);
 }
 
 // Tile plans (measured): up to 4 rows of x arrive as one broadcast line per
@@ -708,7 +705,7 @@ int dispatch_xs_partials(const SkinnyArgs& a, const XsPlan& p, int splits, hipSt
 int dispatch_partials(const SkinnyArgs& a, int splits, hipStream_t s) {
   const int mt = (a.m + kTile - 1) / kTile;
   if (mt > 1) {
-    const XsPlan p = xs_plan(a.m, a.k, a.n);
+    const XsPlan p = xs_plan(a.n, splits);
     if (a.chunks % p.wk == 0) {
       if (mt == 2) return dispatch_xs_partials<2>(a, p, splits, s);
       if (mt == 3) return dispatch_xs_partials<3>(a, p, splits, s);

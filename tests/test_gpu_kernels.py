@@ -147,7 +147,7 @@ def test_add_rms_norm_matches_oracle(rows, cols):
         add_rms_norm(xd, yd[:, : cols // 2].contiguous(), dev(w), 1e-6)
 
 
-@pytest.mark.parametrize("splits,rows", [(1, 3), (4, 16), (8, 64), (8, 5)])
+@pytest.mark.parametrize("splits,rows", [(1, 3), (4, 16), (8, 64), (8, 5), (19, 64), (5, 33)])
 def test_add_rms_norm_split_k_partials(splits, rows):
     g = gen(12)
     x = normal((rows, 2560), g=g)

@@ -172,11 +172,12 @@ def test_silu_mul_random_matches_oracle_and_unfused_path(m, n, k):
     torch.testing.assert_close(got, silu_mul(F.linear(xd, wd)), rtol=2e-2, atol=2e-2)
 
 
-def test_consumers_take_partials_from_the_projection():
+@pytest.mark.parametrize("rows,inner", [(4, 4096), (64, 4096), (64, 9728)])  # 8, 8, 19 splits
+def test_consumers_take_partials_from_the_projection(rows, inner):
     """linear_partials -> add_rms_norm / qkv_norm_rope_cache equals the oracle
     chain bit for bit on integer inputs (the fold is exact there)."""
-    g = gen(180)
-    rows, hidden, inner = 4, 2560, 4096
+    g = gen(180 + rows + inner)
+    hidden = 2560
     attended, wo = ints((rows, inner), -2, 2, g), ints((hidden, inner), -1, 1, g)
     residual = ints((rows, hidden), -8, 8, g)
     gain = normal((hidden,), 1.0, 0.1, g)

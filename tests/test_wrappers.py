@@ -320,23 +320,29 @@ def test_skinny_supports_is_the_reference_static_rule():
 
 
 def test_skinny_split_plan():
-    """The library's plan: a power of two dividing K/64 that leaves every
-    wave a chunk; fewer splits as rows grow (the partials cost rows * splits)."""
+    """The library's plan.  Up to 16 rows: a power of two dividing K/64 that
+    leaves every wave a chunk, fewer as rows grow (the partials cost rows *
+    splits).  Beyond 16 rows: K ranges of at most eight chunks."""
     from starter_amd.kernels import skinny_gemm as sk
     qwen = {"qkv": (6144, 2560), "o": (2560, 4096), "down": (2560, 9728)}
     for n, k in qwen.values():
         prev = None
-        for rows in (1, 4, 16, 32, 64):
+        for rows in (1, 4, 16):
             s = sk.split_count(n, k, rows)
             assert s >= 1 and s & (s - 1) == 0 and (k // 64) % s == 0 and k // 64 // s >= 4
             assert prev is None or s <= prev
             prev = s
+        for rows in (17, 32, 48, 64):
+            s = sk.split_count(n, k, rows)
+            chunks = k // 64
+            assert chunks % s == 0 and chunks // s <= 8
+            assert not any(chunks % t == 0 and chunks // t <= 8 for t in range(1, s))  # the fewest
     assert sk.split_count(6144, 2560, 1) == 8 and sk.split_count(6144, 2560, 16) == 4
     assert sk.split_count(2560, 4096, 1) == 8 and sk.split_count(2560, 9728, 16) == 8
-    # beyond 16 rows (shared-x kernel): the fewest splits giving ~150 workgroups
-    assert [sk.split_count(n, k, 64) for n, k in qwen.values()] == [2, 4, 4]
-    assert sk.split_count(6144, 2560, 32) == 2 and sk.split_count(2560, 4096, 48) == 4
+    assert [sk.split_count(n, k, 64) for n, k in qwen.values()] == [5, 8, 19]
+    assert sk.split_count(6144, 2560, 32) == 5 and sk.split_count(2560, 4096, 48) == 8
     assert sk.split_count(1024, 64, 1) == 1      # one chunk: no split possible
+    assert sk.split_count(1024, 64, 64) == 1
     with pytest.raises(ValueError):
         sk.split_count(6144, 2560, 65)
     with pytest.raises(ValueError):
