@@ -741,21 +741,37 @@ int dispatch_silu(const SkinnyArgs& a, hipStream_t s) {
   }
 }
 
-// Final argmax over a row's workgroup candidates: one workgroup per row.
-__global__ __launch_bounds__(kBlock) void argmax_finalize_kernel(const uint2* cand, int64_t blocks,
-                                                                int64_t* tokens) {
-  __shared__ float wv[kWaves];
-  __shared__ int wi[kWaves];
+// Final argmax over a row's candidates: one 1024-thread workgroup per row,
+// each thread four candidates in flight per round (9,496 candidates for
+// Qwen3-4B: three rounds instead of 37 loads in turn per thread).  The
+// order (larger value, NaN largest, then the lower index) is total, so the
+// reduction order does not change the result.
+constexpr int kFinThreads = 1024;
+constexpr int kFinUnroll = 4;
+__global__ __launch_bounds__(kFinThreads) void argmax_finalize_kernel(const uint2* cand,
+                                                                     int64_t blocks,
+                                                                     int64_t* tokens) {
+  __shared__ float wv[kFinThreads / kWave];
+  __shared__ int wi[kFinThreads / kWave];
   const int64_t row = blockIdx.x;
+  const uint2* c = cand + row * blocks;
   float best = -__builtin_inff();
   int besti = INT32_MAX;
-  for (int64_t j = threadIdx.x; j < blocks; j += kBlock) {
-    const uint2 c = cand[row * blocks + j];
-    const float v = __uint_as_float(c.x);
-    const int i = (int)c.y;
-    if (better(v, i, best, besti)) {
-      best = v;
-      besti = i;
+  for (int64_t j0 = threadIdx.x; j0 < blocks; j0 += (int64_t)kFinThreads * kFinUnroll) {
+    uint2 v[kFinUnroll];
+#pragma unroll
+    for (int u = 0; u < kFinUnroll; ++u) {
+      const int64_t j = j0 + (int64_t)u * kFinThreads;
+      v[u] = j < blocks ? c[j] : make_uint2(__float_as_uint(-__builtin_inff()), (uint32_t)INT32_MAX);
+    }
+#pragma unroll
+    for (int u = 0; u < kFinUnroll; ++u) {
+      const float val = __uint_as_float(v[u].x);
+      const int idx = (int)v[u].y;
+      if (better(val, idx, best, besti)) {
+        best = val;
+        besti = idx;
+      }
     }
   }
 #pragma unroll
@@ -774,7 +790,7 @@ __global__ __launch_bounds__(kBlock) void argmax_finalize_kernel(const uint2* ca
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < kWaves; ++w)
+    for (int w = 1; w < kFinThreads / kWave; ++w)
       if (better(wv[w], wi[w], best, besti)) {
         best = wv[w];
         besti = wi[w];
@@ -838,7 +854,7 @@ extern "C" int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const v
   hipStream_t s = as_stream(stream);
   const int st = dispatch_argmax(a, s);
   if (st != QF_OK) return st;
-  hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)rows), dim3(kBlock), 0, s,
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)rows), dim3(kFinThreads), 0, s,
                      static_cast<const uint2*>(candidates), vocab / kTile, tokens);
   return launch_status();
 }
