@@ -464,6 +464,30 @@ def test_embedding_config5b_full_size():
     assert np.array_equal(bits(out), O.embedding(ids.numpy(), bits(table)))
 
 
+@pytest.mark.parametrize("cols,n_ids", [
+    (2560, 3300),    # 4 rows per wave, whole rows of 5 vectors per lane, ragged last wave
+    (2560, 8195),    # 8 rows per wave, 3 rows left for the last wave
+    (2560, 20000),   # 8 rows per wave, several workgroups per CU
+    (2056, 5000),    # rows of 257 vectors: the last vector of a lane's row is partial
+    (4096, 2100),    # 8 vectors per lane: at most 4 rows per wave
+    (8192, 1100),    # 16 vectors per lane: at most 2 rows per wave
+])
+def test_embedding_streaming_row_plans(cols, n_ids):
+    """Calls of at least 32 MiB stream several rows per wave; every plan, a
+    partial last wave and out-of-range ids match the oracle bit for bit."""
+    g = gen(cols + n_ids)
+    vocab = 4096
+    table = normal((vocab, cols), 0.0, 0.02, g=g)
+    ids = torch.randint(0, vocab, (n_ids,), generator=g)
+    bad = torch.randint(0, n_ids, (64,), generator=g)
+    ids[bad[:32]] = -1
+    ids[bad[32:]] = vocab
+    ids[-1] = 1 << 40
+    out = embedding(dev(ids), dev(table))
+    assert np.array_equal(bits(out), O.embedding(ids.numpy(), bits(table)))
+    assert int(out[-1].count_nonzero()) == 0
+
+
 # ------------------------------------------------------------ rotary tables
 
 def test_rope_tables_match_oracle():
