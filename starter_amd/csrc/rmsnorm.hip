@@ -14,7 +14,9 @@
 // every input byte is read once and every output byte written once.  The sum
 // of squares is reduced in f64 with DPP inside 16-lane rows and ds_bpermute
 // across them; no LDS allocation and no barrier.  Split-K partials (decode)
-// take rms_partials_kernel, one workgroup per row.
+// take rms_partials_kernel, one workgroup per row.  Large calls whose rows are
+// whole multiples of 64 vectors take rms_stream_kernel: several rows per
+// wave, every load (gain included) issued before the first store.
 #include "qf_device.h"
 
 namespace qf {
@@ -132,6 +134,98 @@ __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
   }
 }
 
+// Large calls (MODE 0 or 1, rows of at most 16 vectors per lane): R rows of
+// one wave, with every load issued before the first store - the gain first,
+// then each row's inputs.  gfx950 counts loads and stores on one in-order
+// counter, so a load issued after a store can only be waited for together
+// with that store; here every wait covers older loads only, and row r's
+// arithmetic starts while rows r+1.. are still arriving.  Loads are
+// unconditional (a lane past the row end re-reads the row's last vector and
+// contributes zero), so the compiler has no branch to sink them under.
+template <int VPL, int R, int MODE, bool FULL>
+__device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int lane) {
+  constexpr bool ADD = MODE == 1;
+  const int last = a.nvec - 1;
+  const uint4* wv4 = reinterpret_cast<const uint4*>(a.w);
+  uint4 wv[VPL], xv[R][VPL], bv[R][VPL];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int v = lane + k * kWave;
+    wv[k] = wv4[FULL || v < a.nvec ? v : last];
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint4* xin = reinterpret_cast<const uint4*>(row_base<ADD>(a, row0 + r));
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int v = lane + k * kWave;
+      const int vv = FULL || v < a.nvec ? v : last;
+      xv[r][k] = load16<true>(xin + vv);
+      if constexpr (ADD) {
+        const uint4* bin = reinterpret_cast<const uint4*>(
+            static_cast<const uint16_t*>(a.branch) + (row0 + r) * a.cols);
+        bv[r][k] = load16<true>(bin + vv);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t row = row0 + r;
+    float t[VPL][8];
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int v = lane + k * kWave;
+      const bool on = FULL || v < a.nvec;
+      unpack8(xv[r][k], t[k]);
+      if constexpr (ADD) {
+        float y[8];
+        unpack8(bv[r][k], y);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[k][j] += y[j];
+        const uint4 tv = pack8(t[k]);
+        unpack8(tv, t[k]);
+        if (on) store16<true>(reinterpret_cast<uint4*>(a.total + row * a.cols) + v, tv);
+      }
+      if (!on) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[k][j] = 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += (double)(t[k][j] * t[k][j]);
+    }
+    const float inv = inv_rms(group_sum_f64<kWave>(ss), (float)a.cols, a.eps);
+    uint4* o = reinterpret_cast<uint4*>(a.out + row * a.cols);
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int v = lane + k * kWave;
+      float n[8], w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) n[j] = t[k][j] * inv;
+      round8(n);
+      unpack8(wv[k], w);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) n[j] *= w[j];
+      if (FULL || v < a.nvec) store16<true>(o + v, pack8(n));
+    }
+  }
+}
+
+// One wave per RPW consecutive rows; the grid's last wave, whose rows may run
+// past a.rows, takes its rows one at a time.
+template <int VPL, int RPW, int MODE, bool FULL>
+__global__ __launch_bounds__(kBlock) void rms_stream_kernel(RmsArgs a) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t row0 = __builtin_amdgcn_readfirstlane(
+      ((int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave) * RPW);
+  if (row0 + RPW <= a.rows) {
+    stream_rows<VPL, RPW, MODE, FULL>(a, row0, lane);
+  } else {
+    for (int64_t row = row0; row < a.rows; ++row)  // wave-uniform
+      stream_rows<VPL, 1, MODE, FULL>(a, row, lane);
+  }
+}
+
 // Element value entering the norm: x, or bf16(x + branch) for the add variant.
 template <bool ADD>
 __device__ __forceinline__ float scalar_value(const RmsArgs& a, const uint16_t* x, int64_t row,
@@ -186,10 +280,42 @@ int launch_rows(const RmsArgs& a, hipStream_t s) {
 // Large calls stream with nontemporal accesses and, for rows of at most five
 // vectors per lane (<= 2560 columns) with a bf16 or no branch, two rows per
 // wave; decode-size calls keep one row per wave and cached accesses.
+template <int VPL, int RPW, int MODE>
+int launch_stream(const RmsArgs& a, hipStream_t s) {
+  constexpr int64_t per_block = kBlock / kWave * RPW;
+  const int64_t blocks = (a.rows + per_block - 1) / per_block;
+  hipLaunchKernelGGL((rms_stream_kernel<VPL, RPW, MODE, true>), dim3((unsigned)blocks),
+                     dim3(kBlock), 0, s, a);
+  return launch_status();
+}
+
+// Large calls whose rows are whole multiples of 64 vectors take
+// rms_stream_kernel with the fewest rows per wave (1, 2, 4 or 8, at most 40
+// vectors of each input per lane) that keep the grid within one 4-wave
+// workgroup per CU.  Measured on the [8192, 2560] residual add + norm: 8 rows
+// per wave (256 workgroups) 28.5 us against 29.0 us for rms_vec_kernel's two
+// rows per wave; rows that end mid-vector-group keep rms_vec_kernel, which
+// was faster for them.
+template <int VPL, int MODE>
+int launch_full_stream(const RmsArgs& a, hipStream_t s) {
+  constexpr int kMaxRows = 40 / VPL >= 8 ? 8 : 40 / VPL >= 4 ? 4 : 40 / VPL >= 2 ? 2 : 1;
+  const int64_t waves_per_grid = (int64_t)kCUs * (kBlock / kWave);
+  int rows = 1;
+  while (rows < kMaxRows && (int64_t)rows * waves_per_grid < a.rows) rows *= 2;
+  switch (rows) {
+    case 1: return launch_stream<VPL, 1, MODE>(a, s);
+    case 2: return launch_stream<VPL, (kMaxRows >= 2 ? 2 : 1), MODE>(a, s);
+    case 4: return launch_stream<VPL, (kMaxRows >= 4 ? 4 : 1), MODE>(a, s);
+    default: return launch_stream<VPL, kMaxRows, MODE>(a, s);
+  }
+}
+
 template <int LPR, int VPL, int MODE>
 int launch_vec(const RmsArgs& a, hipStream_t s) {
   const int64_t bytes = a.rows * a.cols * 2 * (MODE == 0 ? 2 : 4);
   if (bytes < kStreamBytes) return launch_rows<LPR, VPL, MODE, 1, false>(a, s);
+  if constexpr (LPR == 64 && MODE != 2)
+    if (a.nvec == VPL * kWave) return launch_full_stream<VPL, MODE>(a, s);
   if constexpr (LPR == 64 && VPL <= 5 && MODE != 2) return launch_rows<LPR, VPL, MODE, 2, true>(a, s);
   return launch_rows<LPR, VPL, MODE, 1, true>(a, s);
 }

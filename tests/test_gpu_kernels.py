@@ -187,6 +187,43 @@ def test_add_rms_norm_config4a_full_size():
     assert_bits_exact(normed, e_normed)
 
 
+@pytest.mark.parametrize("rows,cols", [
+    (1700, 2560),   # 2 rows per wave, partial last wave
+    (3000, 2560),   # 4 rows per wave, partial last wave
+    (8195, 2560),   # 8 rows per wave, 3 rows left for the last wave
+    (20000, 2560),  # 8 rows per wave, several workgroups per CU
+    (1100, 4096),   # 8 vectors per lane: at most 4 rows per wave
+    (2600, 8192),   # 16 vectors per lane: at most 2 rows per wave
+    (2000, 2056),   # rows ending mid-vector-group keep the one-to-two-row kernel
+])
+def test_add_rms_norm_streaming_row_plans(rows, cols):
+    """Calls of at least 32 MiB stream several rows per wave; every plan and a
+    partial last wave match the oracle bit for bit, for both outputs."""
+    g = gen(rows + cols)
+    x, y = normal((rows, cols), g=g), normal((rows, cols), 0.0, 3.0, g=g)
+    w = normal((cols,), 1.0, 0.1, g=g)
+    total, normed = add_rms_norm(dev(x), dev(y), dev(w), 1e-6)
+    e_total, e_normed = O.add_rms_norm(bits(x), bits(y), bits(w), 1e-6)
+    assert np.array_equal(bits(total), e_total)
+    assert_bits_exact(normed, e_normed)
+
+
+@pytest.mark.parametrize("rows,cols", [(3300, 2560), (8195, 2560), (1100, 8192)])
+def test_rms_norm_streaming_row_plans(rows, cols):
+    """Plain RMSNorm through the streaming plans, on a transposed (row-walk) view."""
+    g = gen(rows * 7 + cols)
+    x = normal((rows, cols), g=g)
+    w = normal((cols,), 1.0, 0.1, g=g)
+    half = rows // 2
+    x3 = x[: 2 * half].reshape(2, half, cols)
+    xd = dev(x3).transpose(0, 1)  # rows walk (half, 2): outer stride cols, inner stride half*cols
+    out = rms_norm(xd, dev(w), 1e-6)
+    expected = O.rms_norm(bits(x3.transpose(0, 1).contiguous()), bits(w), 1e-6)
+    assert_bits_exact(out, expected)
+    out = rms_norm(dev(x), dev(w), 1e-6)
+    assert_bits_exact(out, O.rms_norm(bits(x), bits(w), 1e-6))
+
+
 # ----------------------------------------------------------------- silu_mul
 
 @pytest.mark.parametrize("rows,cols", [(1, 9728), (4, 9728), (16, 9728), (3, 512), (2, 96),
