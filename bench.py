@@ -21,8 +21,10 @@ so the figure matches the kernel trace's average duration.  Decode
 configs 1-3 are timed the same way (microseconds per call), and so are the
 split-K decode projections of one Qwen3-4B layer at batch 1-64, beside the
 F.linear (hipBLASLt) path they replace, and decode attention at the engine
-contract's public workloads beside torch's scaled_dot_product_attention.  The CPU baseline is the C oracle
-(single thread) on the same step's shapes, timed on this host.
+contract's public workloads beside torch's scaled_dot_product_attention.  The CPU baseline
+(``cpu_baseline``) is the C oracle (single thread) on the same step's shapes,
+timed on this host; ``cpu_reference`` times every BASELINE config through the
+reference's PyTorch formulas on the host CPU (up to 16 threads, CPU model stated).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
 """
@@ -478,6 +480,124 @@ def cpu_baseline(reps: int = 3) -> dict:
             "cpu": platform.processor() or platform.machine(), "host_cpus": os.cpu_count()}
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def torch_cpu_configs(reps_small: int = 20, reps_large: int = 3) -> dict:
+    """Each BASELINE config through the reference's PyTorch formulas on the
+    host CPU, bf16 tensors as the engine holds them: Qwen3RMSNorm.forward
+    (f32 mean of squares, rsqrt, cast, gain), the residual add, the per-head
+    norm + apply_rotary_pos_emb (rotate-half, cos/sin rows of
+    Qwen3RotaryEmbedding), F.silu(gate) * up and F.embedding.  Threads: the
+    host's cores, at most 16 (one GPU's share of the box).  Median of
+    ``reps`` after one warm-up call.  A reported baseline only."""
+    from torch.nn import functional as F
+
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+
+    def draw(shape, mean=0.0, std=1.0):
+        return (torch.randn(shape, generator=g) * std + mean).to(BF16)
+
+    def norm(x, w, eps=1e-6):
+        f = x.float()
+        f = f * torch.rsqrt(f.pow(2).mean(-1, keepdim=True) + eps)
+        return w * f.to(BF16)
+
+    def rotate_half(x):
+        return torch.cat((-x[..., D // 2:], x[..., : D // 2]), dim=-1)
+
+    def tables(positions):
+        inv = default_inv_freq(5_000_000, D)
+        ang = positions.float()[:, None] * inv[None, :]
+        emb = torch.cat((ang, ang), dim=-1)
+        return emb.cos().to(BF16), emb.sin().to(BF16)
+
+    def timed(fn, reps):
+        fn()
+        samples = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            samples.append(time.perf_counter() - t0)
+        return statistics.median(samples)
+
+    out = {}
+
+    def record(name, seconds, rows, bytes_):
+        out[name] = {"us_per_call": seconds * 1e6, "rows_per_s": rows / seconds,
+                     "gbps": bytes_ / seconds / 1e9}
+
+    with torch.inference_mode():
+        x, w = draw((8, H)), draw((H,), 1.0, 0.1)
+        record("config1_rms_norm_8x2560", timed(lambda: norm(x, w), reps_small), 8,
+               bf16_bytes(2 * 8 * H, H))
+
+        residual, hidden, ws = draw((64, H), 0.0, 4.0), draw((36, 64, H)), draw((36, H), 1.0, 0.1)
+
+        def layers():
+            r = residual
+            for layer in range(36):
+                r = r + hidden[layer]
+                norm(r, ws[layer])
+
+        record("config2_add_rms_norm_64x2560_x36", timed(layers, reps_small) / 36, 64,
+               bf16_bytes(4 * 64 * H, H))
+
+        q, k = draw((32, 1, NQ, D)), draw((32, 1, NK, D))
+        qw, kw = draw((D,), 1.0, 0.1), draw((D,), 1.0, 0.1)
+        cos3, sin3 = tables(torch.randint(0, 32768, (32,), generator=g))
+        cos3, sin3 = cos3.view(32, 1, 1, D), sin3.view(32, 1, 1, D)
+
+        def qk_rope(q, k, cos, sin):
+            qn = norm(q.transpose(1, 2), qw)
+            kn = norm(k.transpose(1, 2), kw)
+            return qn * cos + rotate_half(qn) * sin, kn * cos + rotate_half(kn) * sin
+
+        record("config3_qk_norm_rope_b32", timed(lambda: qk_rope(q, k, cos3, sin3), reps_small),
+               32 * (NQ + NK), bf16_bytes(2 * 32 * (NQ + NK) * D, 2 * D, 2 * 32 * D))
+
+        res4, hid4, w4 = draw((TOKENS, H)), draw((TOKENS, H)), draw((H,), 1.0, 0.1)
+
+        def add_norm():
+            total = res4 + hid4
+            return total, norm(total, w4)
+
+        record("config4a_add_rms_norm_8192x2560", timed(add_norm, reps_large), TOKENS,
+               BYTES["add_rms_norm"])
+
+        q4, k4 = draw((B, T, NQ, D)), draw((B, T, NK, D))
+        cos4, sin4 = tables(torch.arange(T))
+        cos4, sin4 = cos4.view(1, 1, T, D), sin4.view(1, 1, T, D)
+        record("config4b_qk_norm_rope_4x2048", timed(lambda: qk_rope(q4, k4, cos4, sin4), reps_large),
+               TOKENS * (NQ + NK), bf16_bytes(2 * TOKENS * (NQ + NK) * D, 2 * D, 2 * T * D))
+        del res4, hid4, q4, k4
+
+        gate_up = draw((TOKENS, 2 * I))
+        record("config5a_silu_mul_8192x9728",
+               timed(lambda: F.silu(gate_up[:, :I]) * gate_up[:, I:], reps_large), TOKENS,
+               BYTES["silu_mul"])
+        del gate_up
+
+        table = draw((V, H), 0.0, 0.02)
+        ids = torch.randint(0, V, (TOKENS,), generator=g)
+        record("config5b_embedding_8192_ids", timed(lambda: F.embedding(ids, table), reps_large),
+               TOKENS, BYTES["embedding"])
+        del table
+    torch.set_num_threads(previous)
+    return {"threads": threads, "cpu": cpu_model(), "host_cpus": os.cpu_count(),
+            "what": "reference PyTorch formulas on the host CPU (bf16 tensors)", "configs": out}
+
+
 CALIBRATION_BYTES = 256 << 20  # one-way size of the --profile calibration copy
 PMC_SUMMARY = ROOT / "profiles" / "pmc_prefill_kernels.json"
 
@@ -638,6 +758,21 @@ def main() -> int:
     if not args.no_cpu:
         print("bench: CPU baseline (C oracle) ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline()
+        print("bench: reference PyTorch formulas on the CPU, per config ...", file=sys.stderr,
+              flush=True)
+        result["cpu_reference"] = torch_cpu_configs()
+        gpu_us = {"config1_rms_norm_8x2560": decode.get("config1_rms_norm_8x2560", {}).get("us_per_call"),
+                  "config2_add_rms_norm_64x2560_x36":
+                      decode.get("config2_add_rms_norm_64x2560_x36", {}).get("us_per_call"),
+                  "config3_qk_norm_rope_b32": decode.get("config3_qk_norm_rope_b32", {}).get("us_per_call"),
+                  "config4a_add_rms_norm_8192x2560": kernels["add_rms_norm"]["us_per_call_mean"],
+                  "config5a_silu_mul_8192x9728": kernels["silu_mul"]["us_per_call_mean"],
+                  "config5b_embedding_8192_ids": kernels["embedding"]["us_per_call_mean"]}
+        for name, entry in result["cpu_reference"]["configs"].items():
+            if gpu_us.get(name):
+                entry["gpu_us_per_call"] = gpu_us[name]
+            print(f"bench: cpu {name:34s} {entry['us_per_call']:12.1f} us/call "
+                  f"({result['cpu_reference']['threads']} threads)", file=sys.stderr, flush=True)
     print(json.dumps(result), flush=True)
     return 0
 
