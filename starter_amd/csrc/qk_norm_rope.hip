@@ -208,7 +208,11 @@ __device__ __forceinline__ void norm_rope16(const float* x, const float* w, cons
   hi = pack8(left + 8);
 }
 
-template <bool NT, int UPW = kUnitsPerWave, int MIN_WAVES = 1>
+// FULL: every wave's UPW units exist (units % UPW == 0), so the loads and the
+// unit loop carry no bounds branch; measured on the Qwen3-4B 4 x 2048 call
+// 34.0 us against 35.2 us with the checks (a copy with this kernel's loads and
+// stores and no arithmetic takes 33.0 us).
+template <bool NT, bool FULL, int UPW = kUnitsPerWave, int MIN_WAVES = 1>
 __global__ __launch_bounds__(kBlock, MIN_WAVES) void prefill_qkv_unit_kernel(PrefillArgs a) {
   const uint32_t wave =
       __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave);
@@ -227,7 +231,7 @@ __global__ __launch_bounds__(kBlock, MIN_WAVES) void prefill_qkv_unit_kernel(Pre
   uint4 xlo[UPW], xhi[UPW];
 #pragma unroll
   for (int u = 0; u < UPW; ++u) {
-    if (first + u < a.units) {
+    if (FULL || first + u < a.units) {
       const uint16_t* p = src + (int64_t)(first + u) * kRowLanes * kD;
       xlo[u] = load16<NT>(p);
       xhi[u] = load16<NT>(p + kD / 2);
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(kBlock, MIN_WAVES) void prefill_qkv_unit_kernel(Pre
 #pragma unroll
   for (int u = 0; u < UPW; ++u) {
     const uint32_t unit = first + u;
-    if (unit >= a.units) break;  // wave-uniform
+    if (!FULL && unit >= a.units) break;  // wave-uniform
     uint16_t* dst;
     uint4 lo = xlo[u], hi = xhi[u];
     if (unit < a.q_units + a.k_units) {
@@ -435,12 +439,20 @@ extern "C" int qf_prefill_qkv(const void* qkv, int64_t batch, int64_t length, in
     const uint64_t waves = tokens * per_token;
     a.waves = (uint32_t)waves;
     const uint64_t blocks = (waves + kBlock / kWave - 1) / (kBlock / kWave);
-    if ((int64_t)rows * kD * 4 >= kStreamBytes)
-      hipLaunchKernelGGL((prefill_qkv_unit_kernel<true>), dim3((unsigned)blocks), dim3(kBlock), 0, s,
-                         a);
+    const bool stream = (int64_t)rows * kD * 4 >= kStreamBytes;
+    const bool full = a.units % kUnitsPerWave == 0;
+    if (stream && full)
+      hipLaunchKernelGGL((prefill_qkv_unit_kernel<true, true>), dim3((unsigned)blocks),
+                         dim3(kBlock), 0, s, a);
+    else if (stream)
+      hipLaunchKernelGGL((prefill_qkv_unit_kernel<true, false>), dim3((unsigned)blocks),
+                         dim3(kBlock), 0, s, a);
+    else if (full)
+      hipLaunchKernelGGL((prefill_qkv_unit_kernel<false, true>), dim3((unsigned)blocks),
+                         dim3(kBlock), 0, s, a);
     else
-      hipLaunchKernelGGL((prefill_qkv_unit_kernel<false>), dim3((unsigned)blocks), dim3(kBlock), 0,
-                         s, a);
+      hipLaunchKernelGGL((prefill_qkv_unit_kernel<false, false>), dim3((unsigned)blocks),
+                         dim3(kBlock), 0, s, a);
     return launch_status();
   }
   hipLaunchKernelGGL(prefill_qkv_kernel, dim3(blocks_for(rows)), dim3(kBlock), 0, s, a);

@@ -434,9 +434,12 @@ def test_qkv_split_k_partials_and_position_guard():
 @pytest.mark.parametrize("b,t,c,nq,nk", [(1, 3, 11, 32, 8), (2, 33, 41, 32, 8),
                                          (1, 129, 137, 32, 8), (3, 17, 33, 32, 8),
                                          (2, 7, 13, 4, 2), (2, 5, 9, 12, 4), (1, 1, 3, 4, 2),
-                                         (2, 9, 12, 8, 8), (1, 5, 7, 24, 8), (3, 4, 4, 16, 8)])
+                                         (2, 9, 12, 8, 8), (1, 5, 7, 24, 8), (3, 4, 4, 16, 8),
+                                         (1, 2048, 2050, 24, 8)])
 def test_prefill_qkv_matches_oracle(b, t, c, nq, nk):
-    """tests/test_prefill.py:504-522 of the reference."""
+    """tests/test_prefill.py:504-522 of the reference, plus a call large enough
+    to stream whose unit count (5) leaves the last wave of each token half
+    empty."""
     g = gen(51)
     p = normal((b * t, (nq + 2 * nk) * 128), g=g)
     qw, kw = normal((128,), g=g), normal((128,), g=g)
