@@ -142,7 +142,7 @@ __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
 // arithmetic starts while rows r+1.. are still arriving.  Loads are
 // unconditional (a lane past the row end re-reads the row's last vector and
 // contributes zero), so the compiler has no branch to sink them under.
-template <int VPL, int R, int MODE, bool FULL>
+template <int VPL, int R, int MODE, bool FULL, bool NT>
 __device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int lane) {
   constexpr bool ADD = MODE == 1;
   const int last = a.nvec - 1;
@@ -160,11 +160,11 @@ __device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int 
     for (int k = 0; k < VPL; ++k) {
       const int v = lane + k * kWave;
       const int vv = FULL || v < a.nvec ? v : last;
-      xv[r][k] = load16<true>(xin + vv);
+      xv[r][k] = load16<NT>(xin + vv);
       if constexpr (ADD) {
         const uint4* bin = reinterpret_cast<const uint4*>(
             static_cast<const uint16_t*>(a.branch) + (row0 + r) * a.cols);
-        bv[r][k] = load16<true>(bin + vv);
+        bv[r][k] = load16<NT>(bin + vv);
       }
     }
   }
@@ -185,7 +185,7 @@ __device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int 
         for (int j = 0; j < 8; ++j) t[k][j] += y[j];
         const uint4 tv = pack8(t[k]);
         unpack8(tv, t[k]);
-        if (on) store16<true>(reinterpret_cast<uint4*>(a.total + row * a.cols) + v, tv);
+        if (on) store16<NT>(reinterpret_cast<uint4*>(a.total + row * a.cols) + v, tv);
       }
       if (!on) {
 #pragma unroll
@@ -206,23 +206,23 @@ __device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int 
       unpack8(wv[k], w);
 #pragma unroll
       for (int j = 0; j < 8; ++j) n[j] *= w[j];
-      if (FULL || v < a.nvec) store16<true>(o + v, pack8(n));
+      if (FULL || v < a.nvec) store16<NT>(o + v, pack8(n));
     }
   }
 }
 
 // One wave per RPW consecutive rows; the grid's last wave, whose rows may run
 // past a.rows, takes its rows one at a time.
-template <int VPL, int RPW, int MODE, bool FULL>
+template <int VPL, int RPW, int MODE, bool FULL, bool NT = true>
 __global__ __launch_bounds__(kBlock) void rms_stream_kernel(RmsArgs a) {
   const int lane = threadIdx.x % kWave;
   const int64_t row0 = __builtin_amdgcn_readfirstlane(
       ((int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave) * RPW);
   if (row0 + RPW <= a.rows) {
-    stream_rows<VPL, RPW, MODE, FULL>(a, row0, lane);
+    stream_rows<VPL, RPW, MODE, FULL, NT>(a, row0, lane);
   } else {
     for (int64_t row = row0; row < a.rows; ++row)  // wave-uniform
-      stream_rows<VPL, 1, MODE, FULL>(a, row, lane);
+      stream_rows<VPL, 1, MODE, FULL, NT>(a, row, lane);
   }
 }
 
@@ -313,7 +313,19 @@ int launch_full_stream(const RmsArgs& a, hipStream_t s) {
 template <int LPR, int VPL, int MODE>
 int launch_vec(const RmsArgs& a, hipStream_t s) {
   const int64_t bytes = a.rows * a.cols * 2 * (MODE == 0 ? 2 : 4);
-  if (bytes < kStreamBytes) return launch_rows<LPR, VPL, MODE, 1, false>(a, s);
+  if (bytes < kStreamBytes) {
+    // Decode sizes: one row per wave, cached accesses; whole-group rows take
+    // the loads-before-stores kernel.
+    if constexpr (LPR == 64 && MODE != 2) {
+      if (a.nvec == VPL * kWave) {
+        const int64_t blocks = (a.rows + kBlock / kWave - 1) / (kBlock / kWave);
+        hipLaunchKernelGGL((rms_stream_kernel<VPL, 1, MODE, true, false>), dim3((unsigned)blocks),
+                           dim3(kBlock), 0, s, a);
+        return launch_status();
+      }
+    }
+    return launch_rows<LPR, VPL, MODE, 1, false>(a, s);
+  }
   if constexpr (LPR == 64 && MODE != 2)
     if (a.nvec == VPL * kWave) return launch_full_stream<VPL, MODE>(a, s);
   if constexpr (LPR == 64 && VPL <= 5 && MODE != 2) return launch_rows<LPR, VPL, MODE, 2, true>(a, s);
@@ -335,6 +347,9 @@ __global__ __launch_bounds__(MAXT) void rms_partials_kernel(RmsArgs a) {
   const bool on = v < a.nvec;
   const int vi = on ? v : 0;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  // The gain is loaded first: a load issued after the total store below
+  // could only be waited for together with that store (one in-order counter).
+  const uint4 wv = reinterpret_cast<const uint4*>(a.w)[vi];
   const uint4 xv = on ? load16<false>(reinterpret_cast<const uint4*>(a.x + row * a.cols) + vi)
                       : make_uint4(0, 0, 0, 0);
   float y[8], t[8];
@@ -365,7 +380,7 @@ __global__ __launch_bounds__(MAXT) void rms_partials_kernel(RmsArgs a) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) n[j] = t[j] * inv;
   round8(n);
-  unpack8(reinterpret_cast<const uint4*>(a.w)[v], w);
+  unpack8(wv, w);
 #pragma unroll
   for (int j = 0; j < 8; ++j) n[j] *= w[j];
   store16<false>(reinterpret_cast<uint4*>(a.out + row * a.cols) + v, pack8(n));
