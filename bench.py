@@ -231,7 +231,8 @@ def decode_configs(device) -> dict:
     # Config 1: RMSNorm [8, 2560].
     x, w = normal((8, H), g=g), normal((H,), 1.0, 0.1, g)
     us = graph_time(lambda: rms_norm(x, w, 1e-6), 100)
-    out["config1_rms_norm_8x2560"] = {"us_per_call": us, "bytes": bf16_bytes(2 * 8 * H, H)}
+    out["config1_rms_norm_8x2560"] = {"us_per_call": us, "bytes": bf16_bytes(2 * 8 * H, H),
+                                      "rows": 8}
     # Config 2: add + RMSNorm [64, 2560] chained over 36 layers.
     residual = normal((64, H), 0.0, 4.0, g)
     hidden = normal((36, 64, H), g=g)
@@ -245,7 +246,7 @@ def decode_configs(device) -> dict:
 
     us = graph_time(layers, 1) / 36
     out["config2_add_rms_norm_64x2560_x36"] = {"us_per_call": us,
-                                               "bytes": bf16_bytes(4 * 64 * H, H)}
+                                               "bytes": bf16_bytes(4 * 64 * H, H), "rows": 64}
     # Config 3: QK-norm + RoPE, 32 sequences, per-sequence positions in [0, 32767].
     q, k = normal((32, 32, 1, D), g=g), normal((32, 8, 1, D), g=g)
     qw, kw = normal((D,), 1.0, 0.1, g), normal((D,), 1.0, 0.1, g)
@@ -254,8 +255,10 @@ def decode_configs(device) -> dict:
     cos, sin = cos.view(32, 1, D), sin.view(32, 1, D)
     us = graph_time(lambda: qk_norm_rope(q, k, qw, kw, cos, sin, 1e-6, 1e-6), 100)
     out["config3_qk_norm_rope_b32"] = {"us_per_call": us,
-                                       "bytes": bf16_bytes(2 * 32 * 40 * D, 2 * D, 2 * 32 * D)}
+                                       "bytes": bf16_bytes(2 * 32 * 40 * D, 2 * D, 2 * 32 * D),
+                                       "rows": 32 * 40}
     for entry in out.values():
+        entry["rows_per_s"] = entry["rows"] / (entry["us_per_call"] * 1e-6)
         entry["gbps"] = entry["bytes"] / (entry["us_per_call"] * 1e3)
         entry["frac"] = entry["gbps"] / PEAK_GBPS
         entry["under_5us"] = entry["us_per_call"] < 5.0
