@@ -412,12 +412,15 @@ int dispatch(RmsArgs a, bool vec_ok, hipStream_t s) {
     if (MODE == 2 && nv <= 1024 && a.rows <= (int64_t)UINT32_MAX) {
       // 16 partials in flight per thread up to 4096 columns (512 threads);
       // 8 beyond, where 1024 threads leave 128 registers each.
-      // 8 splits (every split-K projection of the engine up to 16 rows) take
-      // an instantiation with the count fixed: its loads issue with no branch
+      // 8 splits (every split-K projection of the engine up to 16 rows, and
+      // o_proj beyond) and 19 (the down projection beyond 16 rows) take
+      // instantiations with the count fixed: their loads issue with no branch
       // between them (10.5 -> 10.2 us per Qwen3-4B add+norm + qkv pair at batch 1).
       const int threads = (nv + kWave - 1) / kWave * kWave;
       if (nv <= 512 && a.splits == 8)
         hipLaunchKernelGGL((rms_partials_kernel<8, 512, 8>), dim3((unsigned)a.rows), dim3(threads), 0, s, a);
+      else if (nv <= 512 && a.splits == 19)
+        hipLaunchKernelGGL((rms_partials_kernel<19, 512, 19>), dim3((unsigned)a.rows), dim3(threads), 0, s, a);
       else if (nv <= 512)
         hipLaunchKernelGGL((rms_partials_kernel<16, 512>), dim3((unsigned)a.rows), dim3(threads), 0, s, a);
       else
