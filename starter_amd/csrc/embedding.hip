@@ -2,10 +2,11 @@
 // builder for gfx950.
 //
 // Embedding: out[i, :] = table[ids[i], :] - the nn.Embedding lookup of
-// engine/decode_step.py:38, engine/prefill.py:34, engine/decode.py:19.  One
-// wave copies one row with 16-byte loads and stores (lane i moves vectors i,
-// i+64, ...); the id is read once per wave with a scalar load.  Rows are copied as raw bits, so
-// the result is bit-exact by construction.  Out-of-range ids give zero rows.
+// engine/decode_step.py:38, engine/prefill.py:34, engine/decode.py:19.  A wave
+// copies one row (decode sizes) or up to 8 consecutive rows (large calls)
+// with 16-byte loads and stores (lane i moves vectors i, i+64, ...); the ids
+// are read with scalar loads.  Rows are copied as raw bits, so the result is
+// bit-exact by construction.  Out-of-range ids give zero rows.
 //
 // Rotary table: the Qwen3 default RoPE table that engine/decode.py:52-59
 // builds from Qwen3RotaryEmbedding.forward:
