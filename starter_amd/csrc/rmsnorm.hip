@@ -14,9 +14,11 @@
 // every input byte is read once and every output byte written once.  The sum
 // of squares is reduced in f64 with DPP inside 16-lane rows and ds_bpermute
 // across them; no LDS allocation and no barrier.  Split-K partials (decode)
-// take rms_partials_kernel, one workgroup per row.  Large calls whose rows are
-// whole multiples of 64 vectors take rms_stream_kernel: several rows per
-// wave, every load (gain included) issued before the first store.
+// take rms_partials_kernel, one workgroup per row.  Rows that are whole
+// multiples of 64 vectors (plain or bf16-branch add) take rms_stream_kernel:
+// every load (gain included) issued before the first store, several rows per
+// wave with nontemporal accesses for large calls, one row per wave with
+// cached accesses for decode sizes.
 #include "qf_device.h"
 
 namespace qf {
@@ -134,9 +136,10 @@ __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
   }
 }
 
-// Large calls (MODE 0 or 1, rows of at most 16 vectors per lane): R rows of
-// one wave, with every load issued before the first store - the gain first,
-// then each row's inputs.  gfx950 counts loads and stores on one in-order
+// MODE 0 or 1, rows of at most 16 vectors per lane: R rows of one wave (R > 1
+// for large calls, NT = nontemporal accesses; R = 1 with cached accesses for
+// decode sizes), with every load issued before the first store - the gain
+// first, then each row's inputs.  gfx950 counts loads and stores on one in-order
 // counter, so a load issued after a store can only be waited for together
 // with that store; here every wait covers older loads only, and row r's
 // arithmetic starts while rows r+1.. are still arriving.  Loads are
