@@ -46,7 +46,7 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from starter_amd.kernels.decode_fused import add_rms_norm, silu_mul  # noqa: E402
+from starter_amd.kernels.decode_fused import add_rms_norm, qkv_norm_rope_cache, silu_mul  # noqa: E402
 from starter_amd.kernels.embedding import embedding  # noqa: E402
 from starter_amd.kernels.prefill import prefill_qkv  # noqa: E402
 from starter_amd.kernels.qk_norm_rope import qk_norm_rope  # noqa: E402
@@ -257,6 +257,27 @@ def decode_configs(device) -> dict:
     out["config3_qk_norm_rope_b32"] = {"us_per_call": us,
                                        "bytes": bf16_bytes(2 * 32 * 40 * D, 2 * D, 2 * 32 * D),
                                        "rows": 32 * 40}
+    # The other fused kernels at decode batch 64 (the north star's < 5 us/call
+    # bound applies to every fused kernel at batch <= 64).
+    gate_up = normal((64, 2 * I), g=g)
+    us = graph_time(lambda: silu_mul(gate_up), 100)
+    out["decode_silu_mul_64x9728"] = {"us_per_call": us, "bytes": bf16_bytes(3 * 64 * I),
+                                      "rows": 64}
+    table = normal((V, H), 0.0, 0.02, g)
+    ids = torch.randint(0, V, (64,), generator=g, device=device)
+    us = graph_time(lambda: embedding(ids, table), 100)
+    out["decode_embedding_64_ids"] = {"us_per_call": us, "bytes": bf16_bytes(2 * 64 * H) + 8 * 64,
+                                      "rows": 64}
+    del table
+    qkv = normal((64, (NQ + 2 * NK) * D), g=g)
+    kc = torch.zeros((64, NK, CAPACITY, D), dtype=BF16, device=device)
+    vc = torch.zeros_like(kc)
+    ctab, stab = rope_tables(default_inv_freq(5_000_000, D), CAPACITY, device=device)
+    pos = torch.tensor([T], device=device)
+    us = graph_time(lambda: qkv_norm_rope_cache(qkv, qw, kw, 1e-6, 1e-6, ctab, stab, pos, kc, vc), 100)
+    out["decode_qkv_norm_rope_cache_b64"] = {
+        "us_per_call": us, "rows": 64 * (NQ + 2 * NK),
+        "bytes": bf16_bytes(64 * (NQ + 2 * NK) * D + 64 * (NQ + 2 * NK) * D, 2 * D, 2 * D) + 8}
     for entry in out.values():
         entry["rows_per_s"] = entry["rows"] / (entry["us_per_call"] * 1e-6)
         entry["gbps"] = entry["bytes"] / (entry["us_per_call"] * 1e3)
