@@ -9,7 +9,10 @@ reference runs:
 
 * prefill (``engine/prefill.py:26-66``): embedding gather, RMSNorm, packed QKV
   projection (hipBLASLt), ``prefill_qkv`` (Q/K norm + RoPE + K/V cache write),
-  causal attention, and the residual-add + RMSNorm / SiLU * up fusions;
+  causal flash attention with grouped K/V heads (torch's fused SDPA kernel, no
+  score matrix in memory), and the residual-add + RMSNorm / SiLU * up fusions;
+  captured once per (batch, prompt length) in a HIP graph and replayed for
+  every prompt of that shape (``engine/prefill.py:65-99``);
 * decode (``engine/decode_step.py:33-64``): the split-K projections whose f32
   partials feed ``add_rms_norm`` and the split-KV decode attention (which
   also does ``qkv_norm_rope_cache``'s Q/K norm, RoPE and cache write in its
@@ -19,11 +22,18 @@ reference runs:
   (batch, capacity) in a HIP graph and replayed with the position and cache
   lengths advanced on the device.
 
+Tokens reach the host as ``engine/decode.py:110-128`` moves them: step k's
+device-to-host copy into pinned memory is queued before step k + 1 is
+launched, so the GPU runs the next step while the host hands out this one.
+
 Weights come from transformers' ``Qwen3ForCausalLM`` - from a local
 checkpoint directory, or randomly initialised from a config - and are packed
-once (Q|K|V and gate|up rows, as ``engine/engine.py:39-47`` packs them).
-Prefill attention runs in float32 with explicit matmuls; everything else is
-bf16.  There is no CPU path: the engine needs a GPU and the HIP library.
+once (Q|K|V and gate|up rows, as ``engine/engine.py:39-47`` packs them); the
+model's own projection modules are re-pointed at row ranges of the packed
+tensors, so no weight is held twice.  One generation state (caches, tables,
+graphs) is kept at a time, for the most recent (batch, prompt length, new
+tokens), as ``engine/engine.py:62-64`` keeps one.  There is no CPU path: the
+engine needs a GPU and the HIP library.
 """
 
 from __future__ import annotations
@@ -31,7 +41,9 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 import torch
+from torch import nn
 from torch.nn import functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from .kernels.decode_fused import add_rms_norm, silu_mul
 from .kernels.embedding import embedding
@@ -63,13 +75,28 @@ class PackedLayer:
     eps_k: float
 
 
+@torch.no_grad()
+def _pack_rows(*modules) -> torch.Tensor:
+    """Concatenate the modules' weights along the output rows and make each
+    module's weight the matching row range of the result (one copy in memory,
+    as engine/qk_norm_rope.py:22-30 does for Q|K|V)."""
+    packed = torch.cat([m.weight for m in modules]).contiguous()
+    start = 0
+    for module in modules:
+        stop = start + module.weight.shape[0]
+        module.weight = nn.Parameter(packed[start:stop], requires_grad=False)
+        start = stop
+    return packed
+
+
 def pack_layer(layer) -> PackedLayer:
-    """Pack a transformers ``Qwen3DecoderLayer`` (any device / dtype kept)."""
+    """Pack a transformers ``Qwen3DecoderLayer`` (any device / dtype kept); its
+    q/k/v and gate/up modules then read the packed storage."""
     attn, mlp = layer.self_attn, layer.mlp
     return PackedLayer(
-        qkv=torch.cat([attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight]).contiguous(),
+        qkv=_pack_rows(attn.q_proj, attn.k_proj, attn.v_proj),
         o=attn.o_proj.weight.contiguous(),
-        gate_up=torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight]).contiguous(),
+        gate_up=_pack_rows(mlp.gate_proj, mlp.up_proj),
         down=mlp.down_proj.weight.contiguous(),
         ln_in=layer.input_layernorm.weight.contiguous(),
         ln_post=layer.post_attention_layernorm.weight.contiguous(),
@@ -82,16 +109,30 @@ def pack_layer(layer) -> PackedLayer:
     )
 
 
+def check_rotary(model) -> None:
+    """The rotary tables are built from ``inv_freq`` alone (the default RoPE);
+    refuse checkpoints whose rotary module scales or reshapes the angles."""
+    rope = model.model.rotary_emb
+    kind = getattr(rope, "rope_type", "default")
+    scaling = float(getattr(rope, "attention_scaling", 1.0))
+    if kind != "default" or scaling != 1.0:
+        raise ValueError(f"the engine implements the default RoPE only, not rope_type {kind!r} "
+                         f"with attention_scaling {scaling}")
+
+
 #: Largest batch whose decode step merges attention segments inside o_proj.
 MERGED_O_BATCH = 1
 
 
 class _State:
-    """Caches, rotary tables and graph buffers for one (batch, capacity)."""
+    """Caches, rotary tables, graphs and host buffers for one (batch, prompt
+    length, new tokens)."""
 
-    def __init__(self, engine: "Engine", batch: int, capacity: int):
+    def __init__(self, engine: "Engine", batch: int, length: int, new_tokens: int):
         dev = engine.device
-        self.batch, self.capacity = batch, capacity
+        capacity = length + new_tokens
+        self.key = (batch, length, new_tokens)
+        self.batch, self.length, self.capacity = batch, length, capacity
         shape = (batch, engine.kv_heads, capacity, HEAD)
         self.keys = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in engine.layers]
         self.values = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in engine.layers]
@@ -102,9 +143,17 @@ class _State:
         self.merged_o = (batch <= MERGED_O_BATCH and self.attention.splits > 1
                          and supports_merged(self.attention.partials, self.attention.stats, batch,
                                              engine.layers[0].o))
+        self.prompt = torch.zeros((batch, length), dtype=torch.int64, device=dev)
         self.tokens = torch.zeros(batch, dtype=torch.int64, device=dev)
         self.position = torch.zeros(1, dtype=torch.int64, device=dev)
         self.used = torch.zeros(batch * engine.kv_heads, dtype=torch.int32, device=dev)
+        # the step whose tokens the host reads, copied into pinned memory
+        self.host = torch.empty(batch, dtype=torch.int64, pin_memory=True)
+        self.ready = torch.cuda.Event()
+        # graphs need the fused LM head (torch's argmax records a memset node)
+        self.graphable = engine.use_graphs and batch <= _lm_head.MAX_ROWS
+        self.prefill_graph = None
+        self.prefill_logits = None
         self.graph = None
         self.logits = None
 
@@ -113,7 +162,10 @@ class Engine:
     """Greedy Qwen3 generation on the fused gfx950 kernels (see module doc)."""
 
     def __init__(self, model_path: str | None = None, *, config=None, seed: int = 0,
-                 device: str | torch.device = "cuda", use_graphs: bool = True):
+                 device: str | torch.device = "cuda", use_graphs: bool = True,
+                 keep_logits: bool = False):
+        """``keep_logits``: also keep each step's bf16 logits in ``last_logits``
+        (a device copy per step; for tests and inspection)."""
         from transformers import Qwen3ForCausalLM
         self.device = torch.device(device)
         if self.device.type != "cuda" or not torch.cuda.is_available():
@@ -128,6 +180,7 @@ class Engine:
         else:
             raise ValueError("give a local checkpoint directory or a Qwen3Config")
         model = model.to(self.device).eval()
+        check_rotary(model)
         cfg = model.config
         self.config = cfg
         self.model = model
@@ -144,8 +197,13 @@ class Engine:
         self.lm_head = model.lm_head.weight
         self.inv_freq = model.model.rotary_emb.inv_freq.float()
         self.use_graphs = use_graphs
-        self._states: dict[tuple[int, int], _State] = {}
+        self.keep_logits = keep_logits
+        self.state: _State | None = None
         self.last_logits = None
+        # One side stream for every warm-up and capture: torch keeps a BLAS
+        # workspace per stream it has run a projection on, for the life of
+        # the process, so a fresh stream per capture would leak one each.
+        self._capture_stream = torch.cuda.Stream(self.device)
 
     # ------------------------------------------------------------ helpers
 
@@ -161,9 +219,12 @@ class Engine:
         return silu_mul(F.linear(normed, gate_up))
 
     def _select(self, normed, tokens):
-        """LM head + greedy choice: writes the tokens, returns the bf16 logits."""
+        """LM head + greedy choice: writes the tokens; returns the bf16 logits
+        when ``keep_logits`` (else None)."""
         if _lm_head.supports(normed, self.lm_head):
-            return _lm_head.lm_head_argmax(normed, self.lm_head, logits=True, tokens=tokens)[1]
+            out = _lm_head.lm_head_argmax(normed, self.lm_head, logits=self.keep_logits,
+                                          tokens=tokens)
+            return out[1] if self.keep_logits else None
         logits = F.linear(normed, self.lm_head)
         tokens.copy_(logits.argmax(-1))
         return logits
@@ -174,32 +235,38 @@ class Engine:
             return nxt.ln_in, nxt.eps_in
         return self.final_norm, self.final_eps
 
-    def _state(self, batch, capacity) -> _State:
-        key = (batch, capacity)
-        if key not in self._states:
-            self._states[key] = _State(self, batch, capacity)
-        return self._states[key]
+    def _state(self, batch, length, new_tokens) -> _State:
+        """The state for this shape; a different shape drops the old state
+        (caches, graphs and their memory pools) before allocating the new."""
+        key = (batch, length, new_tokens)
+        if self.state is None or self.state.key != key:
+            self.state = None
+            self.last_logits = None
+            self.state = _State(self, batch, length, new_tokens)
+        return self.state
 
     # ------------------------------------------------------------ prefill
 
     def _prefill_attention(self, q, keys, values, length):
-        """Causal GQA attention over the prompt in float32: q [B, T, Hq, 128]."""
+        """Causal GQA attention over the prompt: q [B, T, Hq, 128] against the
+        first T cache slots, on torch's fused flash kernel (grouped K/V heads
+        read in place, no score matrix in memory; the math fallback is not
+        allowed).  Returns [B * T, Hq * 128]."""
         batch = q.shape[0]
-        groups = self.q_heads // self.kv_heads
-        qf = q.float().view(batch, length, self.kv_heads, groups, HEAD).permute(0, 2, 3, 1, 4)
-        k = keys[:, :, :length].float().unsqueeze(2)          # [B, Hkv, 1, T, D]
-        v = values[:, :, :length].float().unsqueeze(2)
-        scores = torch.matmul(qf, k.transpose(-1, -2).contiguous()) * self.scale
-        causal = torch.ones(length, length, dtype=torch.bool, device=q.device).tril()
-        scores = scores.masked_fill(~causal, float("-inf"))
-        out = torch.matmul(torch.softmax(scores, dim=-1), v)   # [B, Hkv, G, T, D]
-        return out.permute(0, 3, 1, 2, 4).reshape(batch * length, self.q_heads * HEAD).to(torch.bfloat16)
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            out = F.scaled_dot_product_attention(
+                q.transpose(1, 2), keys[:, :, :length], values[:, :, :length],
+                is_causal=True, scale=self.scale, enable_gqa=True)
+        return out.transpose(1, 2).reshape(batch * length, self.q_heads * HEAD)
 
-    def _prefill(self, st: _State, ids: torch.Tensor):
-        batch, length = ids.shape
-        x = embedding(ids.reshape(-1), self.embed)
+    def _prefill(self, st: _State):
+        """Prompt ``st.prompt`` -> K/V cache slots [0, T) of every layer and the
+        first token of each sequence in ``st.tokens`` (capturable)."""
+        batch, length = st.batch, st.length
+        x = embedding(st.prompt.view(-1), self.embed)
         first = self.layers[0]
         normed = rms_norm(x, first.ln_in, first.eps_in)
+        last = len(self.layers) - 1
         for index, layer in enumerate(self.layers):
             q = prefill_qkv(F.linear(normed, layer.qkv), layer.q_norm, layer.k_norm, layer.eps_q,
                             layer.eps_k, st.cos, st.sin, st.keys[index], st.values[index], length)
@@ -207,9 +274,34 @@ class Engine:
             x, normed = add_rms_norm(x, F.linear(attended, layer.o), layer.ln_post, layer.eps_post)
             hidden = silu_mul(F.linear(normed, layer.gate_up))
             weight, eps = self._next_norm(index)
+            if index == last:
+                # only each sequence's last position feeds the LM head
+                x = x.view(batch, length, -1)[:, -1].contiguous()
+                hidden = hidden.view(batch, length, -1)[:, -1].contiguous()
             x, normed = add_rms_norm(x, F.linear(hidden, layer.down), weight, eps)
-        last = normed.view(batch, length, -1)[:, -1].contiguous()
-        return self._select(last, st.tokens)
+        return self._select(normed, st.tokens)
+
+    def _run_prefill(self, st: _State):
+        """Prefill from a HIP graph captured on the first prompt of this shape
+        (warm-up runs first, then capture, then the replay that produces the
+        result), as engine/prefill.py:79-99 does; eager when graphs are off."""
+        if not st.graphable:
+            return self._prefill(st)
+        if st.prefill_graph is None:
+            current = torch.cuda.current_stream(self.device)
+            stream = self._capture_stream
+            stream.wait_stream(current)
+            with torch.cuda.stream(stream):
+                for _ in range(2):
+                    self._prefill(st)
+            current.wait_stream(stream)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                st.prefill_logits = self._prefill(st)
+            current.wait_stream(stream)
+            st.prefill_graph = graph
+        st.prefill_graph.replay()
+        return st.prefill_logits
 
     # ------------------------------------------------------------- decode
 
@@ -244,7 +336,7 @@ class Engine:
         the first step (same token, same slot), so they leave the caches as
         the first replay does; the buffers are restored before replaying."""
         saved = (st.tokens.clone(), st.position.clone(), st.used.clone())
-        stream = torch.cuda.Stream(self.device)
+        stream = self._capture_stream
         stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(stream):
             for _ in range(2):
@@ -263,26 +355,32 @@ class Engine:
     @torch.inference_mode()
     def generate(self, input_ids: list[list[int]], max_new_tokens: int):
         """Greedy continuation; yields one list[int] per step, max_new_tokens times."""
-        if max_new_tokens < 1 or not input_ids:
-            raise ValueError("need at least one sequence and one new token")
+        if max_new_tokens <= 0:
+            return
+        if not input_ids:
+            raise ValueError("need at least one sequence")
         length = len(input_ids[0])
         if length < 1 or any(len(row) != length for row in input_ids):
             raise ValueError("every sequence in input_ids must have the same non-zero length")
         batch = len(input_ids)
-        st = self._state(batch, length + max_new_tokens)
-        ids = torch.tensor(input_ids, dtype=torch.int64, device=self.device)
-        self.last_logits = self._prefill(st, ids)
-        yield st.tokens.tolist()
-        if max_new_tokens == 1:
-            return
+        st = self._state(batch, length, max_new_tokens)
+        st.prompt.copy_(torch.tensor(input_ids, dtype=torch.int64))
+        logits = self._run_prefill(st)
         st.position.fill_(length)
         st.used.fill_(length + 1)
-        if self.use_graphs and st.graph is None:
+        if max_new_tokens > 1 and st.graphable and st.graph is None:
             self._capture(st)
-        for _ in range(max_new_tokens - 1):
-            if self.use_graphs:
-                st.graph.replay()
-                self.last_logits = st.logits
-            else:
-                self.last_logits = self._decode_step(st)
-            yield st.tokens.tolist()
+        for step in range(max_new_tokens):
+            # queue this step's tokens for the host, then the next step
+            st.host.copy_(st.tokens, non_blocking=True)
+            if self.keep_logits:
+                self.last_logits = logits.clone()
+            st.ready.record()
+            if step + 1 < max_new_tokens:
+                if st.graph is not None:
+                    st.graph.replay()
+                    logits = st.logits
+                else:
+                    logits = self._decode_step(st)
+            st.ready.synchronize()
+            yield st.host.tolist()

@@ -5,9 +5,13 @@
 * ``PackedMLP`` - engine/mlp.py:8-21: one packed ``[2I, H]`` gate/up weight;
   on CUDA bf16 the activation is the fused ``silu_mul`` kernel on the packed
   projection, elsewhere it is the reference module's own ``act_fn(gate) * up``.
+* ``DecodeQKNormRoPE`` - engine/qk_norm_rope.py:10-71: a ``Qwen3Attention``
+  whose single-token decode forward runs the per-head Q/K RMSNorm and the
+  rotary embedding as one ``kernels.qk_norm_rope`` launch; every other call
+  (prefill, CPU, training, unusual rotary layouts) is the model's own forward.
 * ``FusedEmbedding`` - embedding gather that shares ``embed_tokens.weight``.
 * ``install(model)`` - the module swaps ``Engine.__init__`` performs
-  (engine/engine.py:39-46) for norms, MLPs and the embedding.
+  (engine/engine.py:39-47) for norms, MLPs, attention and the embedding.
 """
 
 from __future__ import annotations
@@ -16,11 +20,15 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
+from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+from transformers.models.qwen3.modeling_qwen3 import Qwen3Attention, eager_attention_forward
+
 from .kernels.decode_fused import silu_mul
 from .kernels.embedding import FusedEmbedding
+from .kernels.qk_norm_rope import HEAD, qk_norm_rope
 from .kernels.rmsnorm import rms_norm
 
-__all__ = ["FusedRMSNorm", "PackedMLP", "FusedEmbedding", "install"]
+__all__ = ["FusedRMSNorm", "PackedMLP", "DecodeQKNormRoPE", "FusedEmbedding", "install"]
 
 
 class FusedRMSNorm(nn.Module):
@@ -58,8 +66,85 @@ class PackedMLP(nn.Module):
         return self.down_proj(self.act_fn(gate) * up)
 
 
+class DecodeQKNormRoPE(Qwen3Attention):
+    """``Qwen3Attention`` with the decode-step Q/K norm + RoPE fused.
+
+    Shares every submodule and attribute of the attention it wraps (no weight
+    is allocated or initialised), and packs the three input projections into
+    one ``qkv_weight`` ``[(Hq + 2 Hkv) * 128, H]`` whose row ranges become the
+    q/k/v modules' weights, so the state dict and the prefill path read the
+    same storage as the packed decode step (engine/qk_norm_rope.py:11-30).
+    """
+
+    _COPIED = ("config", "layer_idx", "layer_type", "head_dim", "num_key_value_groups",
+               "scaling", "attention_dropout", "is_causal", "sliding_window", "q_proj",
+               "k_proj", "v_proj", "o_proj", "q_norm", "k_norm")
+
+    @torch.no_grad()
+    def __init__(self, reference):
+        nn.Module.__init__(self)
+        for name in self._COPIED:
+            if hasattr(reference, name):
+                setattr(self, name, getattr(reference, name))
+        self.train(reference.training)
+        self.qkv_weight = torch.cat((self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
+        start = 0
+        for module in (self.q_proj, self.k_proj, self.v_proj):
+            stop = start + module.weight.shape[0]
+            module.weight = nn.Parameter(self.qkv_weight[start:stop], requires_grad=False)
+            start = stop
+
+    def _fused(self, hidden_states, cos, sin, cache, kwargs) -> bool:
+        """True when the one-token kernel applies.  Reads shapes, dtypes and
+        flags only (no device values), so the decision is capturable; the
+        rules follow engine/qk_norm_rope.py:37-51, except that a missing
+        attention mask does not force the fallback (transformers 5 passes
+        none for an unpadded single-token step under SDPA)."""
+        return not (
+            hidden_states.ndim != 3 or hidden_states.shape[1] != 1
+            or not hidden_states.is_cuda or hidden_states.dtype != torch.bfloat16
+            or self.head_dim != HEAD or self.training
+            or getattr(cache, "prefilling", False)
+            or kwargs.get("output_attentions", False)
+            or self.config._attn_implementation not in ("sdpa", "eager", "starter_decode_gqa")
+            or cos.ndim != 3 or cos.shape != sin.shape
+            or cos.shape[0] not in (1, hidden_states.shape[0])
+            or tuple(cos.shape[1:]) != (1, HEAD)
+            or cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16
+            or any(m.bias is not None for m in (self.q_proj, self.k_proj, self.v_proj))
+        )
+
+    def forward(self, hidden_states, position_embeddings, attention_mask,
+                past_key_values=None, **kwargs):
+        # transformers 4.x passes the cache as ``past_key_value``.
+        legacy = kwargs.pop("past_key_value", None)
+        if past_key_values is None:
+            past_key_values = legacy
+        cos, sin = position_embeddings
+        if not self._fused(hidden_states, cos, sin, past_key_values, kwargs):
+            return super().forward(hidden_states, position_embeddings, attention_mask,
+                                   past_key_values=past_key_values, **kwargs)
+        batch = hidden_states.shape[0]
+        nq = self.q_proj.weight.shape[0] // HEAD
+        nk = self.k_proj.weight.shape[0] // HEAD
+        # One packed projection; q, k and v are [B, H, 1, 128] views of its rows.
+        qkv = F.linear(hidden_states, self.qkv_weight).view(batch, nq + 2 * nk, 1, HEAD)
+        q, k, v = qkv[:, :nq], qkv[:, nq:nq + nk], qkv[:, nq + nk:]
+        q, k = qk_norm_rope(q, k, self.q_norm.weight, self.k_norm.weight, cos, sin,
+                            self.q_norm.variance_epsilon, self.k_norm.variance_epsilon)
+        if past_key_values is not None:
+            k, v = past_key_values.update(k, v, self.layer_idx)
+        interface = ALL_ATTENTION_FUNCTIONS.get_interface(self.config._attn_implementation,
+                                                          eager_attention_forward)
+        output, weights = interface(self, q, k, v, attention_mask, dropout=0.0,
+                                    scaling=self.scaling, sliding_window=self.sliding_window,
+                                    **kwargs)
+        return self.o_proj(output.reshape(batch, 1, -1).contiguous()), weights
+
+
 def install(model):
-    """Swap a Qwen3ForCausalLM's norms, MLPs and embedding for the fused modules."""
+    """Swap a Qwen3ForCausalLM's norms, MLPs, attention and embedding for the
+    fused modules (the swaps of engine/engine.py:39-47)."""
     base = model.model
     base.embed_tokens = FusedEmbedding(base.embed_tokens)
     base.norm = FusedRMSNorm(base.norm)
@@ -69,4 +154,5 @@ def install(model):
         layer.self_attn.q_norm = FusedRMSNorm(layer.self_attn.q_norm)
         layer.self_attn.k_norm = FusedRMSNorm(layer.self_attn.k_norm)
         layer.mlp = PackedMLP(layer.mlp)
+        layer.self_attn = DecodeQKNormRoPE(layer.self_attn)
     return model

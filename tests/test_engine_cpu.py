@@ -29,6 +29,21 @@ def test_pack_layer_row_order():
     assert torch.equal(packed.down, mlp.down_proj.weight) and torch.equal(packed.o, attn.o_proj.weight)
     assert packed.eps_q == attn.q_norm.variance_epsilon
     assert all(t.is_contiguous() for t in (packed.qkv, packed.gate_up, packed.o, packed.down))
+    # the modules now read row ranges of the packed tensors (one copy in memory)
+    size = packed.qkv.element_size()
+    for w, start in ((attn.q_proj.weight, 0), (attn.k_proj.weight, 4 * 128),
+                     (attn.v_proj.weight, 6 * 128)):
+        assert w.data_ptr() == packed.qkv.data_ptr() + start * 256 * size
+    assert mlp.gate_proj.weight.data_ptr() == packed.gate_up.data_ptr()
+    assert mlp.up_proj.weight.data_ptr() == packed.gate_up.data_ptr() + 512 * 256 * size
+
+
+def test_rotary_check():
+    engine.check_rotary(Qwen3ForCausalLM(Qwen3Config(**TINY)))
+    scaled = dict(TINY, rope_scaling={"rope_type": "yarn", "factor": 4.0,
+                                      "original_max_position_embeddings": 4096})
+    with pytest.raises(ValueError):
+        engine.check_rotary(Qwen3ForCausalLM(Qwen3Config(**scaled)))
 
 
 def test_engine_needs_a_gpu():

@@ -9,6 +9,12 @@ native ones (rtol 0.02, atol 0.125), its token may trail the native argmax by
 at most 2.0 logits, and wherever the native top two differ by more than 0.25
 it must be the native argmax.  Graph replay must equal eager stepping bit for bit,
 and a local safetensors checkpoint must give the same generation.
+
+The contract cases of tests/test_qk_norm_rope.py:201-220 in the reference
+((3, 7, 5) twice, (1, 1, 3), (2, 13, 1), (2, 13, 0)): exactly ``count``
+lists of ``batch`` ids, each token within 2.0 logits of the native maximum
+over the engine's own prefix.  Switching shapes keeps one state, so device
+memory does not grow with the number of shapes seen.
 """
 
 from __future__ import annotations
@@ -42,7 +48,7 @@ def run(engine, prompts, steps):
 
 @pytest.fixture(scope="module")
 def engine():
-    return Engine(config=Qwen3Config(**TINY), seed=3)
+    return Engine(config=Qwen3Config(**TINY), seed=3, keep_logits=True)
 
 
 @pytest.mark.parametrize("batch,length,steps", [(1, 5, 6), (1, 70, 4), (3, 37, 5), (4, 64, 4)])
@@ -64,23 +70,75 @@ def test_generation_matches_native_teacher_forced(engine, batch, length, steps):
     assert torch.equal(tokens[clear], expected.argmax(-1)[clear])
     assert bool(clear.any())
     if (batch, length) == (1, 70):  # two key segments: o_proj merges them itself
-        assert engine._states[(1, length + steps)].merged_o
+        assert engine.state.merged_o
 
 
 def test_graph_replay_equals_eager(engine):
     prompts = [[7, 8, 9, 10, 11, 12, 13], [1, 2, 3, 4, 5, 6, 7]]
     graph_tokens, graph_logits = run(engine, prompts, 5)
-    eager = Engine(config=Qwen3Config(**TINY), seed=3, use_graphs=False)
+    eager = Engine(config=Qwen3Config(**TINY), seed=3, use_graphs=False, keep_logits=True)
     eager_tokens, eager_logits = run(eager, prompts, 5)
     assert torch.equal(graph_tokens, eager_tokens)
     assert torch.equal(graph_logits, eager_logits)
-    # a second call of the same shape reuses the captured graph and caches
-    again_tokens, _ = run(engine, prompts, 5)
-    assert torch.equal(again_tokens, graph_tokens)
+    # a second call of the same shape replays both captured graphs
+    graphs = (engine.state.prefill_graph, engine.state.graph)
+    assert all(g is not None for g in graphs)
+    again_tokens, again_logits = run(engine, prompts, 5)
+    assert torch.equal(again_tokens, graph_tokens) and torch.equal(again_logits, graph_logits)
+    assert (engine.state.prefill_graph, engine.state.graph) == graphs
+    # new prompt content of the same shape: the replayed prefill reads it
+    other = [[99, 98, 97, 96, 95, 94, 93], [3, 1, 4, 1, 5, 9, 2]]
+    new_tokens, new_logits = run(engine, other, 5)
+    eager_tokens, eager_logits = run(eager, other, 5)
+    assert torch.equal(new_tokens, eager_tokens) and torch.equal(new_logits, eager_logits)
+    assert not torch.equal(new_logits, graph_logits)
 
 
 def test_local_checkpoint(engine, tmp_path):
     engine.model.save_pretrained(tmp_path, safe_serialization=True)
-    loaded = Engine(str(tmp_path))
+    loaded = Engine(str(tmp_path), keep_logits=True)
     prompts = [[5, 4, 3, 2, 1, 0, 9, 8]]
     assert torch.equal(run(loaded, prompts, 4)[0], run(engine, prompts, 4)[0])
+
+
+def _own_prefix_gap(model, prompt, emitted):
+    """Largest gap between the native maximum and the emitted token's logit,
+    the native model scoring the prompt plus the engine's own tokens."""
+    length = len(prompt[0])
+    tokens = torch.tensor(emitted).T                          # [B, count]
+    own = torch.cat([torch.tensor(prompt), tokens[:, :-1]], dim=1)
+    with torch.inference_mode():
+        logits = model(input_ids=own).logits[:, length - 1:].float()
+    gap = logits.amax(-1) - logits.gather(-1, tokens[..., None]).squeeze(-1)
+    assert bool(torch.isfinite(gap).all())
+    return float(gap.max())
+
+
+def test_contract_shapes(engine):
+    native = copy.deepcopy(engine.model).float().cpu()
+    g = torch.Generator().manual_seed(31)
+    for batch, length, count in ((3, 7, 5), (3, 7, 5), (1, 1, 3), (2, 13, 1), (2, 13, 0)):
+        prompt = torch.randint(0, TINY["vocab_size"], (batch, length), generator=g).tolist()
+        emitted = list(engine.generate(prompt, count))
+        assert len(emitted) == count
+        if count == 0:
+            continue
+        assert all(len(row) == batch and all(isinstance(t, int) for t in row) for row in emitted)
+        assert _own_prefix_gap(native, prompt, emitted) <= 2.0
+
+
+def test_one_state_at_a_time():
+    """Shapes A, B, A, B: the second visit of a shape holds the same device
+    memory as the first (the previous state and its graphs are released)."""
+    engine = Engine(config=Qwen3Config(**TINY), seed=5)
+    shapes = ((2, 40, 6), (4, 100, 9))
+    seen = {}
+    for _ in range(2):
+        for batch, length, count in shapes:
+            prompt = [[(7 * i + j) % TINY["vocab_size"] for j in range(length)] for i in range(batch)]
+            assert len(list(engine.generate(prompt, count))) == count
+            torch.cuda.synchronize()
+            seen.setdefault((batch, length, count), []).append(torch.cuda.memory_allocated())
+            assert engine.state.key == (batch, length, count)
+    for first, second in seen.values():
+        assert second <= first
