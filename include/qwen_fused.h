@@ -35,6 +35,7 @@ extern "C" {
 #define QF_E_ARG (-1)     /* null pointer, negative size, bad stride */
 #define QF_E_SHAPE (-2)   /* unsupported shape (e.g. head width != 128) */
 #define QF_E_ALIGN (-3)   /* pointer alignment the selected path needs */
+#define QF_E_CAPACITY (-4) /* input larger than a static scratch buffer holds */
 
 /* Library version: major*10000 + minor*100 + patch. */
 int qf_version(void);
@@ -303,6 +304,26 @@ int64_t qf_lm_head_blocks(int64_t vocab);
  */
 int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const void* weight, int64_t vocab,
                       void* candidates, int64_t* tokens, void* logits, void* stream);
+
+/* 8-byte candidate slots in qf_lm_head_argmax_static's scratch (8 MiB per GPU). */
+#define QF_LM_HEAD_STATIC_SLOTS (1 << 20)
+
+/*
+ * qf_lm_head_argmax without the caller's candidate buffer and without any
+ * allocation: the candidates live in a static device array of
+ * QF_LM_HEAD_STATIC_SLOTS slots, one per GPU, held until the process ends.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, results and status codes as
+ * qf_lm_head_argmax minus `candidates`; QF_E_CAPACITY when
+ * rows * qf_lm_head_blocks(vocab) exceeds QF_LM_HEAD_STATIC_SLOTS (64 rows
+ * of a vocabulary up to 262,144).  Calls that overlap on one GPU (other
+ * streams or threads) share the array and race: order them on one stream.
+ * The first call on a device looks the array's address up (a host call,
+ * no allocation) and keeps it.
+ */
+int qf_lm_head_argmax_static(const void* x, int64_t rows, int64_t k, const void* weight,
+                             int64_t vocab, int64_t* tokens, void* logits, void* stream);
 
 #ifdef __cplusplus
 }

@@ -214,6 +214,7 @@ extern "C" const char* qf_error_string(int status) {
     case QF_E_ARG: return "invalid argument (null pointer, negative size or stride)";
     case QF_E_SHAPE: return "unsupported shape";
     case QF_E_ALIGN: return "pointer or stride not aligned for the kernel";
+    case QF_E_CAPACITY: return "input exceeds the static scratch capacity";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

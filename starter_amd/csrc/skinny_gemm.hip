@@ -43,6 +43,8 @@
 // equal the exactly rounded dot product whenever every partial sum is an
 // exactly representable f32 (e.g. integer inputs below 2^24), and otherwise
 // differ from it by f32 accumulation error only.
+#include <mutex>
+
 #include "qf_device.h"
 #include "qf_merge.h"
 #include "qf_silu.h"
@@ -832,16 +834,29 @@ extern "C" int64_t qf_lm_head_blocks(int64_t vocab) {
   return vocab > 0 && vocab % kTile == 0 ? vocab / kTile : QF_E_SHAPE;
 }
 
-extern "C" int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const void* weight,
-                                 int64_t vocab, void* candidates, int64_t* tokens, void* logits,
-                                 void* stream) {
+namespace qf {
+namespace {
+// Host checks of the LM head arguments other than the candidate buffer.
+int lm_head_status(const void* x, int64_t rows, int64_t k, const void* weight, int64_t vocab,
+                   const int64_t* tokens, const void* logits) {
   if (rows < 1 || rows > kMaxRows || k <= 0 || k % kChunk != 0 || k > (int64_t)INT32_MAX ||
       vocab <= 0 || vocab % kTile != 0 || vocab > (int64_t)INT32_MAX / 2)
     return QF_E_SHAPE;
-  if (!x || !weight || !candidates || !tokens) return QF_E_ARG;
-  if (!aligned16(x) || !aligned16(weight) || (reinterpret_cast<uintptr_t>(candidates) & 7u) != 0 ||
-      (reinterpret_cast<uintptr_t>(logits) & 7u) != 0)
+  if (!x || !weight || !tokens) return QF_E_ARG;
+  if (!aligned16(x) || !aligned16(weight) || (reinterpret_cast<uintptr_t>(logits) & 7u) != 0)
     return QF_E_ALIGN;
+  return QF_OK;
+}
+}  // namespace
+}  // namespace qf
+
+extern "C" int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const void* weight,
+                                 int64_t vocab, void* candidates, int64_t* tokens, void* logits,
+                                 void* stream) {
+  const int checked = lm_head_status(x, rows, k, weight, vocab, tokens, logits);
+  if (checked != QF_OK) return checked;
+  if (!candidates) return QF_E_ARG;
+  if ((reinterpret_cast<uintptr_t>(candidates) & 7u) != 0) return QF_E_ALIGN;
   SkinnyArgs a;
   a.x = static_cast<const uint16_t*>(x);
   a.w = static_cast<const uint16_t*>(weight);
@@ -857,6 +872,59 @@ extern "C" int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const v
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)rows), dim3(kFinThreads), 0, s,
                      static_cast<const uint2*>(candidates), vocab / kTile, tokens);
   return launch_status();
+}
+
+// Candidate scratch of qf_lm_head_argmax_static: a file-scope device array,
+// one copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device
+// address): each device's address comes from hipGetSymbolAddress, taken once
+// per device with that device current, and only that address is used.
+static __device__ __align__(256) uint2 scratch[QF_LM_HEAD_STATIC_SLOTS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices] = {};
+
+// This device's address of `scratch` (nullptr and a status on failure).
+void* scratch_address(int* status) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *status = static_cast<int>(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *status = QF_E_ARG;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      *status = e != hipSuccess ? static_cast<int>(e) : QF_E_ARG;
+      return nullptr;
+    }
+    g_scratch[dev] = ptr;
+  }
+  *status = QF_OK;
+  return g_scratch[dev];
+}
+}  // namespace
+
+extern "C" int qf_lm_head_argmax_static(const void* x, int64_t rows, int64_t k,
+                                        const void* weight, int64_t vocab, int64_t* tokens,
+                                        void* logits, void* stream) {
+  const int checked = lm_head_status(x, rows, k, weight, vocab, tokens, logits);
+  if (checked != QF_OK) return checked;
+  if (rows * (vocab / kTile) > QF_LM_HEAD_STATIC_SLOTS) return QF_E_CAPACITY;
+  int status = QF_OK;
+  void* candidates = scratch_address(&status);
+  if (candidates == nullptr) return status;
+  // Every candidate slot the finalize kernel reads is written first by the
+  // projection's epilogue, so nothing left by an earlier call is read.
+  return qf_lm_head_argmax(x, rows, k, weight, vocab, candidates, tokens, logits, stream);
 }
 
 extern "C" int qf_linear_splits(int64_t rows, int64_t k, int64_t n) {

@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 19
+    assert len(names) == 20
 
 
 def test_library_exports_every_symbol():
@@ -46,6 +46,7 @@ def test_version_and_error_strings():
     assert b"invalid argument" in lib.qf_error_string(-1)
     assert b"shape" in lib.qf_error_string(-2)
     assert b"aligned" in lib.qf_error_string(-3)
+    assert b"static scratch" in lib.qf_error_string(-4)
     assert lib.qf_error_string(-99) == b"unknown status"
 
 
@@ -99,6 +100,15 @@ def test_host_side_argument_errors_launch_nothing():
     assert lib.qf_lm_head_argmax(bogus, 1, 2560, bogus, 151930, bogus, bogus, None, None) == -2
     assert lib.qf_lm_head_argmax(bogus, 1, 2560, bogus, 151936, None, bogus, None, None) == -1
     assert lib.qf_lm_head_argmax(bogus + 8, 1, 2560, bogus, 151936, bogus, bogus, None, None) == -3
+    # the allocation-free variant checks the same arguments, then its capacity
+    # (64 rows x 16,384 blocks fit; one more vocabulary tile does not)
+    static = lib.qf_lm_head_argmax_static
+    assert static(bogus, 65, 2560, bogus, 151936, bogus, None, None) == -2
+    assert static(bogus, 1, 2560, bogus, 151930, bogus, None, None) == -2
+    assert static(bogus, 1, 2560, bogus, 151936, None, None, None) == -1
+    assert static(bogus + 8, 1, 2560, bogus, 151936, bogus, None, None) == -3
+    assert static(bogus, 64, 2560, bogus, 16 * 16385, bogus, None, None) == -4
+    assert static(bogus, 65, 2560, bogus, 16 * 16384, bogus, None, None) == -2
     # decode attention: group size, split plan, scale, alignment
     split, span = ctypes.c_int32(), ctypes.c_int64()
     assert lib.qf_attention_partition(0, 64, 256, ctypes.byref(split), ctypes.byref(span)) == -1
