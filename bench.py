@@ -22,9 +22,10 @@ configs 1-3 are timed the same way (microseconds per call), and so are the
 split-K decode projections of one Qwen3-4B layer at batch 1-64, beside the
 F.linear (hipBLASLt) path they replace, and decode attention at the engine
 contract's public workloads beside torch's scaled_dot_product_attention.  The CPU baseline
-(``cpu_baseline``) is the C oracle (single thread) on the same step's shapes,
-timed on this host; ``cpu_reference`` times every BASELINE config through the
-reference's PyTorch formulas on the host CPU (up to 16 threads, CPU model stated).
+(``cpu_baseline``) is the whole step through the reference's PyTorch formulas
+on the host CPU (up to 16 threads, CPU model stated); ``cpu_reference`` also
+times every BASELINE config that way, and ``cpu_baseline_oracle`` is the C
+oracle (one thread) on the step's shapes.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
 """
@@ -510,7 +511,7 @@ def cpu_baseline(reps: int = 3) -> dict:
     return {"value": step_bytes / seconds / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"C oracle, whole 4x2048-token step (4 kernels), median of {reps} reps "
                       f"after 1 warmup: {seconds * 1e3:.0f} ms/step",
-            "cpu": platform.processor() or platform.machine(), "host_cpus": os.cpu_count()}
+            "cpu": cpu_model(), "host_cpus": os.cpu_count()}
 
 
 def cpu_model() -> str:
@@ -625,10 +626,36 @@ def torch_cpu_configs(reps_small: int = 20, reps_large: int = 3) -> dict:
         ids = torch.randint(0, V, (TOKENS,), generator=g)
         record("config5b_embedding_8192_ids", timed(lambda: F.embedding(ids, table), reps_large),
                TOKENS, BYTES["embedding"])
-        del table
+
+        # The GPU step's four calls on its shapes: gather, add + norm, the
+        # packed Q|K|V row's head norm + RoPE with the K and V cache fill
+        # (engine/prefill.py:34-51), SiLU * up.
+        res4, hid4 = draw((TOKENS, H)), draw((TOKENS, H))
+        qkv = draw((TOKENS, (NQ + 2 * NK) * D))
+        keys = torch.zeros((B, NK, CAPACITY, D), dtype=BF16)
+        values = torch.zeros_like(keys)
+        gate_up = draw((TOKENS, 2 * I))
+
+        def step():
+            F.embedding(ids, table)
+            total = res4 + hid4
+            norm(total, w4)
+            heads = qkv.view(B, T, NQ + 2 * NK, D).transpose(1, 2)      # [B, H, T, D]
+            qn, kn = norm(heads[:, :NQ], qw), norm(heads[:, NQ:NQ + NK], kw)
+            q = qn * cos4 + rotate_half(qn) * sin4
+            keys[:, :, :T] = kn * cos4 + rotate_half(kn) * sin4
+            values[:, :, :T] = heads[:, NQ + NK:]
+            F.silu(gate_up[:, :I]) * gate_up[:, I:]
+            return q
+
+        step_s = timed(step, reps_large)
+        del table, gate_up, qkv, keys, values, res4, hid4
     torch.set_num_threads(previous)
+    step_bytes = sum(BYTES.values())
     return {"threads": threads, "cpu": cpu_model(), "host_cpus": os.cpu_count(),
-            "what": "reference PyTorch formulas on the host CPU (bf16 tensors)", "configs": out}
+            "what": "reference PyTorch formulas on the host CPU (bf16 tensors)", "configs": out,
+            "step": {"seconds": step_s, "bytes": step_bytes, "gbps": step_bytes / step_s / 1e9,
+                     "reps": reps_large}}
 
 
 CALIBRATION_BYTES = 256 << 20  # one-way size of the --profile calibration copy
@@ -789,11 +816,21 @@ def main() -> int:
         "copy_gbps": copy_gbps,
     }
     if not args.no_cpu:
-        print("bench: CPU baseline (C oracle) ...", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline()
-        print("bench: reference PyTorch formulas on the CPU, per config ...", file=sys.stderr,
-              flush=True)
-        result["cpu_reference"] = torch_cpu_configs()
+        print("bench: reference PyTorch formulas on the CPU, per config and whole step ...",
+              file=sys.stderr, flush=True)
+        reference = torch_cpu_configs()
+        result["cpu_reference"] = reference
+        step = reference["step"]
+        result["cpu_baseline"] = {
+            "value": step["gbps"], "unit": "GB/s", "cores": reference["threads"], "kind": "port",
+            "sample": (f"the reference's PyTorch formulas (Qwen3RMSNorm, residual add, per-head "
+                       f"norm + apply_rotary_pos_emb with the K/V cache fill, F.silu(gate) * up, "
+                       f"F.embedding) on bf16 CPU tensors, the whole 4 x 2048-token step, "
+                       f"{reference['threads']} threads, median of {step['reps']} after one "
+                       f"warm-up: {step['seconds'] * 1e3:.1f} ms/step"),
+            "cpu": reference["cpu"], "host_cpus": reference["host_cpus"]}
+        print("bench: CPU baseline (C oracle, one thread) ...", file=sys.stderr, flush=True)
+        result["cpu_baseline_oracle"] = cpu_baseline()
         gpu_us = {"config1_rms_norm_8x2560": decode.get("config1_rms_norm_8x2560", {}).get("us_per_call"),
                   "config2_add_rms_norm_64x2560_x36":
                       decode.get("config2_add_rms_norm_64x2560_x36", {}).get("us_per_call"),

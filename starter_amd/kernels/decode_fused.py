@@ -90,16 +90,19 @@ def silu_mul(gate_up, block=1024):
 
 def qkv_norm_rope_cache(qkv, q_weight, k_weight, q_eps, k_eps, cos, sin, position,
                         key_cache, value_cache):
-    """Normalize and rotate packed Q/K, write K/V rows into slot ``position``.
+    """Decode step's Q/K head RMSNorm + RoPE with the K/V cache write.
 
-    ``qkv`` is BF16 [batch, (Nq + 2 Nkv) * D] from one packed projection, or
-    FP32 split-K partials [S, batch, (Nq + 2 Nkv) * D] of it, added and rounded
-    once to BF16 inside the kernel. ``cos`` and ``sin`` are [capacity, D] tables
-    for every absolute slot; ``position`` is one int64 device value and is the
-    only slot of ``key_cache``/``value_cache`` ([batch, Nkv, capacity, D]) that
-    is mutated. Returns fresh Q [batch, Nq, 1, D].  D must be 128.
-    Mirrors engine/kernels/decode_fused.py:172-210.  A position outside
-    [0, capacity) leaves the caches untouched and yields an all-NaN Q.
+    Input: one packed projection row per sequence, ``[q heads | k heads |
+    v heads]`` of 128 each - bf16 ``[batch, width]``, or the f32 split-K
+    partials ``[S, batch, width]`` that the kernel sums in order and rounds to
+    bf16 first.  The rotary angle comes from row ``position`` of the
+    ``[capacity, 128]`` cos/sin tables, with ``position`` an int64 ``(1,)``
+    tensor read on the device.  The normalised, rotated key row and the copied
+    value row go to slot ``position`` of ``key_cache`` / ``value_cache``
+    (``[batch, Nkv, capacity, 128]``); no other slot changes.  Returns a new
+    ``[batch, Nq, 1, 128]`` Q.  Contract of engine/kernels/decode_fused.py:
+    172-210; unlike it, a position outside [0, capacity) writes nothing and
+    the returned Q is all NaN.
     """
     if qkv.ndim == 3 and qkv.dtype == torch.float32:
         if not qkv.is_cuda or not qkv.is_contiguous() or qkv.shape[0] < 1:

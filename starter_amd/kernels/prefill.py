@@ -16,12 +16,15 @@ HEAD = 128
 
 
 def prefill_qkv(qkv, qw, kw, qeps, keps, cos, sin, keys, values, length):
-    """Read packed BF16 [B*T,(Hq+2Hkv)*128]; overwrite only cache [:,:,:T].
+    """Prompt-wide Q/K head RMSNorm + RoPE with the K/V cache fill.
 
-    Angles are the model-generated [C,128] tables already owned by DecodeState.
-    Return a fresh, contiguous BF16 Q [B,T,Hq,128]. All tensors share a device.
-    This is a full fresh prefill at position zero, not chunked prefill.
-    Mirrors engine/kernels/prefill.py:66-96.
+    ``qkv`` holds one packed ``[q heads | k heads | v heads]`` row per prompt
+    token (bf16 ``[B * T, (Hq + 2 Hkv) * 128]``); token t of a sequence sits
+    at position t, so its angles are row t of the ``[C, 128]`` cos/sin tables.
+    Keys (normalised and rotated) and values (copied) fill slots [0, T) of the
+    ``[B, Hkv, C, 128]`` caches and nothing else; the inputs are not written.
+    Returns a new contiguous bf16 Q ``[B, T, Hq, 128]``.  Every tensor on one
+    device.  Contract of engine/kernels/prefill.py:66-96.
     """
     if keys.ndim != 4 or values.shape != keys.shape:
         raise ValueError("K/V must have matching [B,Hkv,C,D] shapes")

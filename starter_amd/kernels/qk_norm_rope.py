@@ -23,11 +23,16 @@ def _rows_view(t: torch.Tensor):
 
 
 def qk_norm_rope(q, k, q_weight, k_weight, cos, sin, q_eps, k_eps):
-    """Read-only BF16 inputs; return fresh contiguous Q/K, [B,H,1,128].
+    """One-token Q/K head RMSNorm + RoPE: returns new contiguous bf16 Q and K
+    of shape ``[B, H, 1, 128]``.
 
-    Q/K may be strided; gains must be [128]. Cos/sin are [1 or B,1,128]
-    from the existing rotary embedding, NOT recomputed or cached here.
-    Mirrors engine/kernels/qk_norm_rope.py:47-73.
+    ``q`` and ``k`` (bf16 ``[B, H, 1, 128]``) may be strided views, such as
+    head slices of one packed projection; they are read in place when their
+    head rows are 16-byte aligned.  ``q_weight`` / ``k_weight`` are the
+    ``[128]`` gains; ``cos`` / ``sin`` are the rotary rows the model already
+    computed, ``[1, 1, 128]`` (shared) or ``[B, 1, 128]`` (per sequence).
+    Nothing is written to the inputs.  Contract of
+    engine/kernels/qk_norm_rope.py:47-73.
     """
     batch = q.shape[0]
     if (q.ndim != 4 or k.ndim != 4 or tuple(q.shape[2:]) != (1, HEAD)

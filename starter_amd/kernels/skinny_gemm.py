@@ -57,10 +57,13 @@ def supports(x, weight, pairs=False):
 
 
 def split_count(n, k, rows=1):
-    """K splits of ``linear_partials`` for x [rows, k] @ W[n, k].T (a power of two).
+    """K splits of ``linear_partials`` for x [rows, k] @ W[n, k].T.
 
-    The plan lives in the library (qf_linear_splits) so C callers get the same
-    one; compare engine/kernels/skinny_gemm.py:86-91, which ignores rows.
+    Each split covers an equal run of whole 64-wide k chunks, so the count
+    divides k / 64: a power of two up to 16 rows; beyond, K ranges of about
+    512 per workgroup (5, 8 and 19 splits on the Qwen3-4B shapes).  The plan
+    lives in the library (qf_linear_splits) so C callers get the same one;
+    compare engine/kernels/skinny_gemm.py:86-91, which ignores rows.
     """
     status = _lib.lib().qf_linear_splits(int(rows), int(k), int(n))
     if status < 1:
