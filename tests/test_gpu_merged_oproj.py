@@ -8,6 +8,16 @@ bit, with the same caches.  Covered: one and two batches of segments
 (S = 2..32), batch 1..16 (16 is the most rows), group widths 1, 4 and 16,
 heads with no valid key (zero rows), and a HIP graph replayed with the
 position advanced on the device.
+
+Against the oracle directly: the oracle's Q/K/V fold, norm, RoPE and cache
+write, its float64 attention rounded to bf16, then its exactly rounded
+partials of that attended row.  The attention has no bit-exact target (the
+bf16 probabilities make it tile-order dependent), so each partial must lie
+within sum_k |W[n, k]| * |a_hip[k] - a_oracle[k]| (what the attention
+differences can move it) plus the f32 accumulation bound 2^-16 *
+sum_k |W[n, k] * a[k]| of the oracle's, with a_hip within the reference's
+attention tolerance of a_oracle; the caches must equal the oracle's bit for
+bit.
 """
 
 from __future__ import annotations
@@ -15,7 +25,9 @@ from __future__ import annotations
 import pytest
 import torch
 
-from conftest import assert_bits_exact, gen, normal
+import numpy as np
+
+from conftest import O, assert_bits_exact, bits, gen, normal
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
@@ -132,3 +144,47 @@ def test_graph_replays_follow_the_device_position():
             assert_bits_exact(kg, ke, f"key cache after replay {replay}")
             position.add_(1)
             used.add_(1)
+
+
+@pytest.mark.parametrize("b,hq,hk,cap,n,rule", [CASES[0], CASES[3], CASES[4], CASES[6]])
+def test_merged_projection_against_the_oracle(b, hq, hk, cap, n, rule):
+    qkv, qw, kw, k, v, w = operands(b, hq, hk, cap, n, 1900 + cap + b)
+    pos = cap - 1
+    if rule == "full":
+        used = torch.full((b * hk,), cap, dtype=torch.int32)
+    else:
+        used = torch.arange(b * hk, dtype=torch.int32) * 97 % (cap + 1)
+        used[-1] = 0
+        used[0] = cap
+    cos, sin = rope_tables(INV_FREQ, cap, device=DEV)
+    plan = SmallQueryAttention(b, hq, hk, cap, DEV)
+    kh, vh = k.clone(), v.clone()
+    position = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    with torch.inference_mode():
+        plan.run_qkv_unmerged(qkv, qw, kw, 1e-6, 2e-6, cos, sin, position, kh, vh,
+                              used.to(DEV), SCALE)
+        out = linear_partials_merged(plan.partials, plan.stats, b, w)
+        # the attended row the merge produced, for the bound below
+        attended = plan.run_qkv(qkv, qw, kw, 1e-6, 2e-6, cos, sin, position, k.clone(),
+                                v.clone(), used.to(DEV), SCALE)
+    torch.cuda.synchronize()
+    q_or, k_or, v_or = O.qkv_norm_rope_cache(qkv.cpu().numpy(), bits(qw), bits(kw), 1e-6, 2e-6,
+                                             bits(cos), bits(sin), pos, bits(k), bits(v))
+    assert_bits_exact(kh, k_or, "key cache vs oracle")
+    assert_bits_exact(vh, v_or, "value cache vs oracle")
+    att_or = O.decode_attention(q_or, k_or, v_or, used.numpy(), SCALE)      # bf16 [B, 1, Hq, 128]
+    a_or = O.bf16_value(att_or.reshape(b, -1)).astype(np.float64)
+    a_hip = O.bf16_value(bits(attended).reshape(b, -1)).astype(np.float64)
+    np.testing.assert_allclose(a_hip, a_or, rtol=0.02, atol=0.004)
+    splits = out.shape[0]
+    want = O.linear_partials(att_or.reshape(b, -1), bits(w), splits).astype(np.float64)
+    got = out.cpu().numpy().astype(np.float64)
+    wv = np.abs(O.bf16_value(bits(w)).astype(np.float64))                # [N, K]
+    span = (hq * 128) // splits
+    for s_ in range(splits):
+        cols = slice(s_ * span, (s_ + 1) * span)
+        moved = np.abs(a_hip[:, cols] - a_or[:, cols]) @ wv[:, cols].T     # [B, N]
+        accum = 2.0 ** -16 * (np.abs(a_or[:, cols]) @ wv[:, cols].T)
+        err = np.abs(got[s_] - want[s_])
+        assert bool((err <= moved + accum + 1e-30).all()), (
+            f"split {s_}: worst excess {float((err - moved - accum).max()):.3g}")
