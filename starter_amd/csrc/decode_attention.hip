@@ -17,8 +17,8 @@
 // in unused cache slots stay invisible.
 //
 // Groups of up to 4 query rows (Qwen3-4B's 4) take attn_mfma_kernel, which
-// computes the scores on the matrix cores (see there); wider groups take
-// attn_kernel, all on the VALU, described next.
+// computes both the scores and P V on the matrix cores (see there); wider
+// groups take attn_kernel, all on the VALU, described next.
 //
 // Layout (HBM-bound: every K/V byte of the used prefix is read once, ~4
 // flops per byte): a wave reads 4 consecutive keys per 16-byte load - 16
@@ -412,37 +412,48 @@ __global__ __launch_bounds__(W * kWave) void attn_kernel(AttnArgs a) {
 
 // Matrix-core variant for groups of at most 4 query rows (Qwen3: 4), the
 // same contract and results within the kernels' bf16 rounding of the
-// probabilities.  Each wave takes 16-key blocks w, w+4, ... of the segment:
-// S = Q K^T of a block is one chain of four v_mfma_f32_16x16x32_bf16 (A = the
-// query rows, zero-padded to 16; B = the 16 keys, lane l reading key l % 16,
-// dims 8*(l/16) + 32s, straight from the cache), which leaves S[q][key] in
-// lanes 0..15.  The wave keeps one running maximum per query (a 16-lane DPP
-// maximum per block), so its four lane groups can later be summed without
-// rescaling; the bf16 probabilities reach the PV layout (lane group per key,
-// lane r holding dims 8r..8r+8, as in attn_kernel) through ds_bpermute, and
-// PV stays f32 FMAs.  Compared with attn_kernel this removes the per-key dot
-// products and their 16-lane sums from the VALU.
+// probabilities and f32 accumulation order.  Each wave takes 16-key blocks
+// w, w+4, ... of the segment, and both products run on the matrix cores:
+//
+// * Scores, transposed: S^T = K Q^T of a block is one chain of four
+//   v_mfma_f32_16x16x32_bf16 (A = the 16 keys, lane l reading key l % 16,
+//   dims 8 (l / 16) + 32 s straight from the cache; B = the query rows,
+//   zero-padded to 16).  That leaves lane l holding S[query l % 16][keys
+//   4 (l / 16) + i], i < 4: exactly the A operand of
+//   v_mfma_f32_16x16x16_bf16 for P V with the keys along k, so the bf16
+//   probabilities need no cross-lane moves.
+// * P V: the block's V rows go to the wave's LDS buffer in their own
+//   key-major layout (288-byte rows: at most two-way bank conflicts for the
+//   reads below), and ds_read_b64_tr_b16 - lane i of each 16-lane group
+//   receives element i % 4 of the 8 bytes that lanes 4q + i / 4 address,
+//   q = 0..3 - turns lane 4q + t's address of dims 16 db + 4t .. +4 of key
+//   4 (l / 16) + q into the B operand (key 4 (l / 16) + q, dim 16 db + l % 16).
+//   Eight MFMAs cover the 128 dims; lanes 0..15 accumulate O[query i][16 db + l].
+//
+// Each lane keeps the running maximum and the f32 denominator of its own
+// query over its own keys (the four lanes of a query share the maximum, a
+// two-step shuffle reduction per block); the accumulators of a query are
+// rescaled when its maximum moves (a wave-uniform test of the four
+// queries' factors).  The four waves' totals are merged through LDS.
+// Measured against the earlier form of this kernel (scores Q K^T on the
+// matrix cores, P V on the VALU as packed bf16 dot products after
+// ds_bpermute moves of the probabilities) on the engine's shapes: batch 1 x
+// 545 keys 9.58 -> 8.67 us, 4 x 2081 14.35 -> 13.50, 16 x 641 15.36 ->
+// 14.61, 64 x 1024 47.40 -> 45.89 us.  Three or four sets in flight are
+// 5-25% slower than two.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float dpp_max16(float x) {
-  x = fmaxf(x, __uint_as_float(dpp_u32<kQuadXor1>(__float_as_uint(x))));
-  x = fmaxf(x, __uint_as_float(dpp_u32<kQuadXor2>(__float_as_uint(x))));
-  x = fmaxf(x, __uint_as_float(dpp_u32<kRowHalfMirror>(__float_as_uint(x))));
-  x = fmaxf(x, __uint_as_float(dpp_u32<kRowMirror>(__float_as_uint(x))));
-  return x;
-}
-// Lane 0's value in every lane (all lanes active).
-__device__ __forceinline__ float first_lane(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
-}
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+constexpr int kVRow = 288;  // LDS bytes per staged V key row (256 + 32 pad)
 
 template <int GT, bool FUSED, bool NTL = false, int NS = 2>
 __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
   static_assert(GT == 1 || GT == 2 || GT == 4, "query rows per kv head");
   constexpr int kW = kBlock / kWave;
-  __shared__ float xm[kW - 1][GT], xl[kW - 1][GT];
-  __shared__ float xacc[kW - 1][GT][kD];
+  __shared__ float xm[kW][GT], xl[kW][GT];
+  __shared__ float xacc[kW][GT][kD];
+  __shared__ __attribute__((aligned(16))) uint8_t vlds[kW][16 * kVRow];
   __shared__ uint4 qs[FUSED ? GT : 1][16], kvs[2][16];
   const int vh = blockIdx.x;
   const int seg = blockIdx.y;
@@ -467,7 +478,8 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
   const int n = nb > wave ? (int)((nb - wave + kW - 1) / kW) : 0;
   const int64_t last_key = end - 1;  // a valid slot whenever n > 0
 
-  // Query rows as the MFMA A operand: row = lane % 16 (< G), k = dims 8*(lane/16) + 32 s.
+  // Query rows as the scores' B operand: column = lane % 16 (< G), k = dims
+  // 8*(lane/16) + 32 s.
   uint4 qa[4];
   if constexpr (!FUSED) {
 #pragma unroll
@@ -509,14 +521,14 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
     }
   }
 
-  float m[GT], l[GT], acc[GT][8];
+  // This lane's query r: running maximum and partial denominator over the
+  // lane's keys; O in tiles of 16 dims (lanes 0..15: O[query i][16 db + r]).
+  float mq = kNegInf, lq = 0.0f;
+  f32x4 oacc[8];
 #pragma unroll
-  for (int g = 0; g < GT; ++g) {
-    m[g] = kNegInf;
-    l[g] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
-  }
+  for (int db = 0; db < 8; ++db) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint8_t* vb = vlds[wave];
+  const int rd = (4 * q4 + (r >> 2)) * kVRow + 8 * (r & 3);  // transpose-read address
   auto consume = [&](int d, int j) {
     const int64_t b0 = start + (int64_t)(wave + kW * j) * 16;
     if constexpr (FUSED) {
@@ -533,69 +545,53 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
     f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[s]),
-                                                   __builtin_bit_cast(bf16x8, kf[d][s]), c, 0, 0, 0);
-    // Lanes 0..15 hold S[q = i][key b0 + lane]; other rows are padding.
-    const bool on = b0 + r < end;
-    float sc[GT], mn[GT], corr[GT];
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[d][s]),
+                                                   __builtin_bit_cast(bf16x8, qa[s]), c, 0, 0, 0);
+    float sc[4], bm = kNegInf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool on = r < rows && b0 + 4 * q4 + i < end;
+      sc[i] = on ? c[i] * a.scale_log2 : kNegInf;
+      bm = fmaxf(bm, sc[i]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    const float mn = fmaxf(mq, bm);
+    const float corr = mn == kNegInf ? 1.0f : exp2_hw(mq - mn);
+    float p[4], ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = mn == kNegInf ? 0.0f : exp2_hw(sc[i] - mn);  // 0 for a masked key or row
+      ps += p[i];
+    }
+    lq = lq * corr + ps;
+    mq = mn;
+    float cq[GT];
     bool rescale = false;
 #pragma unroll
-    for (int i = 0; i < GT; ++i) {
-      sc[i] = on ? c[i] * a.scale_log2 : kNegInf;
-      mn[i] = fmaxf(m[i], first_lane(dpp_max16(sc[i])));
-      corr[i] = mn[i] == kNegInf ? 1.0f : exp2_hw(m[i] - mn[i]);
-      rescale |= corr[i] != 1.0f;
+    for (int g = 0; g < GT; ++g) {
+      cq[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), g));
+      rescale |= cq[g] != 1.0f;
     }
     if (rescale) {  // wave-uniform
 #pragma unroll
-      for (int g = 0; g < GT; ++g) {
-        l[g] *= corr[g];
+      for (int db = 0; db < 8; ++db)
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) acc[g][jj] *= corr[g];
-      }
+        for (int g = 0; g < GT; ++g) oacc[db][g] *= cq[g];
     }
-    float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < GT; ++i) {
-      p[i] = mn[i] == kNegInf ? 0.0f : exp2_hw(sc[i] - mn[i]);  // 0 for a masked key
-      l[i] += p[i];  // partial over this lane's keys (lanes 0..15 count)
-      m[i] = mn[i];
+    for (int u = 0; u < 4; ++u)
+      *reinterpret_cast<uint4*>(vb + (q4 + 4 * u) * kVRow + 16 * r) = vf[d][u];
+    wave_lds_fence();
+    // The probabilities are rounded to bf16 before they multiply V.
+    const v4i16 pa = __builtin_bit_cast(v4i16, make_uint2(pack2(p[0], p[1]), pack2(p[2], p[3])));
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const v4i16 vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_v4i16*)((__attribute__((address_space(3))) uint8_t*)vb + rd + 32 * db));
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vt, oacc[db], 0, 0, 0);
     }
-    const uint32_t p01 = pack2(p[0], p[1]), p23 = pack2(p[2], p[3]);
-    // PV on packed bf16: this lane's keys q4 + 4u in pairs (u = 0, 1 and
-    // 2, 3); v_perm_b32 pairs the two keys' probabilities per query row and
-    // their values per dimension, and one v_dot2_f32_bf16 adds both
-    // products (half the VALU work of f32 FMAs on unpacked values).
-    uint32_t b01[4], b23[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int src = (q4 + 4 * u) * 4;  // byte address of the lane holding key q4 + 4u
-      b01[u] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)p01);
-      b23[u] = 0;
-      if constexpr (GT == 4) b23[u] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)p23);
-    }
-    constexpr uint32_t kLoPair = 0x05040100u, kHiPair = 0x07060302u;  // (x.lo, y.lo), (x.hi, y.hi)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int u0 = 2 * h, u1 = 2 * h + 1;
-      bf16x2 pp[4];
-      pp[0] = __builtin_bit_cast(bf16x2, __builtin_amdgcn_perm(b01[u1], b01[u0], kLoPair));
-      pp[1] = __builtin_bit_cast(bf16x2, __builtin_amdgcn_perm(b01[u1], b01[u0], kHiPair));
-      pp[2] = __builtin_bit_cast(bf16x2, __builtin_amdgcn_perm(b23[u1], b23[u0], kLoPair));
-      pp[3] = __builtin_bit_cast(bf16x2, __builtin_amdgcn_perm(b23[u1], b23[u0], kHiPair));
-      const uint32_t va[4] = {vf[d][u0].x, vf[d][u0].y, vf[d][u0].z, vf[d][u0].w};
-      const uint32_t vb[4] = {vf[d][u1].x, vf[d][u1].y, vf[d][u1].z, vf[d][u1].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x2 vlo = __builtin_bit_cast(bf16x2, __builtin_amdgcn_perm(vb[j], va[j], kLoPair));
-        const bf16x2 vhi = __builtin_bit_cast(bf16x2, __builtin_amdgcn_perm(vb[j], va[j], kHiPair));
-#pragma unroll
-        for (int g = 0; g < GT; ++g) {
-          acc[g][2 * j] = __builtin_amdgcn_fdot2_f32_bf16(pp[g], vlo, acc[g][2 * j], false);
-          acc[g][2 * j + 1] = __builtin_amdgcn_fdot2_f32_bf16(pp[g], vhi, acc[g][2 * j + 1], false);
-        }
-      }
-    }
+    wave_lds_fence();  // the reads complete before the next block's writes
   };
   if (n > 0) {
     for (int i = 0;; i += NS) {
@@ -612,50 +608,42 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
     }
   }
 
-  // Wave totals (one maximum per wave): l over the 16 key lanes of row 0,
-  // acc over the four lane groups.
-  State<GT> st;
-#pragma unroll
-  for (int g = 0; g < GT; ++g) {
-    float t = l[g];
-    t += __uint_as_float(dpp_u32<kQuadXor1>(__float_as_uint(t)));
-    t += __uint_as_float(dpp_u32<kQuadXor2>(__float_as_uint(t)));
-    t += __uint_as_float(dpp_u32<kRowHalfMirror>(__float_as_uint(t)));
-    t += __uint_as_float(dpp_u32<kRowMirror>(__float_as_uint(t)));
-    st.l[g] = first_lane(t);
-    st.m[g] = m[g];
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      float v = acc[g][jj];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      st.acc[g][jj] = v;
-    }
+  // Wave totals through LDS: query g's maximum and denominator (summed over
+  // its four key lanes) from lane g, O rows from lanes 0..15; wave 0's lanes
+  // 0..15 then take query g's dims 8r..8r+8 of every wave, in wave order.
+  float lt = lq + __shfl_xor(lq, 16);
+  lt += __shfl_xor(lt, 32);
+  if (lane < GT) {
+    xm[wave][lane] = mq;
+    xl[wave][lane] = lt;
   }
-  if (wave > 0 && lane < 16) {
+  if (q4 == 0) {
 #pragma unroll
-    for (int g = 0; g < GT; ++g) {
-      if (lane == 0) {
-        xm[wave - 1][g] = st.m[g];
-        xl[wave - 1][g] = st.l[g];
-      }
+    for (int db = 0; db < 8; ++db)
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) xacc[wave - 1][g][8 * r + jj] = st.acc[g][jj];
-    }
+      for (int g = 0; g < GT; ++g) xacc[wave][g][16 * db + r] = oacc[db][g];
   }
   __syncthreads();
-  const bool owner = wave == 0 && lane < 16;
-  if (owner) {
+  State<GT> st;
+  if (wave == 0 && lane < 16) {
 #pragma unroll
-    for (int w = 0; w < kW - 1; ++w)
+    for (int g = 0; g < GT; ++g) {
+      st.m[g] = xm[0][g];
+      st.l[g] = xl[0][g];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) st.acc[g][jj] = xacc[0][g][8 * r + jj];
+    }
+#pragma unroll
+    for (int w = 1; w < kW; ++w)
 #pragma unroll
       for (int g = 0; g < GT; ++g) {
-        float oacc[8];
+        float o8[8];
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) oacc[jj] = xacc[w][g][8 * r + jj];
-        merge_row<GT>(st, g, xm[w][g], xl[w][g], oacc);
+        for (int jj = 0; jj < 8; ++jj) o8[jj] = xacc[w][g][8 * r + jj];
+        merge_row<GT>(st, g, xm[w][g], xl[w][g], o8);
       }
   }
+  const bool owner = wave == 0 && lane < 16;
   if (a.splits == 1) {
     if (!owner) return;
 #pragma unroll

@@ -62,6 +62,15 @@ __device__ __forceinline__ void round8(float* f) {
   unpack8(u, f);
 }
 
+// Orders one wave's LDS writes before its reads of other lanes' data (and the
+// reads before the next writes); LDS executes a wave's operations in order,
+// so this costs no instruction.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ---- 16-byte global loads / stores ------------------------------------------
 
 // NT = true marks the access nontemporal (streamed once: the "nt" bit of

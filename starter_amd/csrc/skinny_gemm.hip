@@ -104,15 +104,6 @@ __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, const f32x
                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// Orders one wave's LDS writes before its reads of other lanes' data (and the
-// reads before the next writes); LDS executes a wave's operations in order,
-// so this costs no instruction.
-__device__ __forceinline__ void wave_lds_fence() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // Staging tiles: 128-byte rows, 16-byte piece c of row r stored at piece
 // c ^ ((r >> 1) & 7).  Both access patterns then touch 16 distinct 16-byte
 // bank groups per 16 lanes: the chunk loads' writes (rows r, r + 1, all
