@@ -138,6 +138,28 @@ int qf_prefill_qkv(const void* qkv, int64_t batch, int64_t length, int32_t nq,
                    void* value_cache, void* stream);
 
 /*
+ * Causal attention of a fresh prompt over its own K/V cache slots, grouped
+ * query heads (G = q_heads / kv_heads query heads per KV head).  Replaces the
+ * prefill's call of torch's dense causal flash attention,
+ * engine/prefill.py:13-23 (_native_attention: aten._flash_attention_forward
+ * with is_causal on q and the cache views k/v[:, :, :length]):
+ *   out[b, t, h] = bf16( softmax_{j <= t}((q[b,t,h] . k[b, h/G, j]) * scale)
+ *                        @ v[b, h/G, j] )
+ * with f32 scores and running softmax statistics, the probabilities rounded
+ * to bf16 before they multiply V, and the f32 result divided by its f32
+ * denominator once.
+ *   q:   bf16 [batch, length, q_heads, 128] (the layout qf_prefill_qkv writes)
+ *   key_cache/value_cache: bf16 [batch, kv_heads, capacity, 128]; slots
+ *        [0, length) are read, nothing at or past `length` is attended.
+ *   out: bf16 [batch, length, q_heads, 128]
+ * G must be 1, 2, 4 or 8 (QF_E_SHAPE otherwise); every pointer 16-byte
+ * aligned.  One launch (matrix-core scores and P V, keys staged in LDS).
+ */
+int qf_prefill_attention(const void* q, const void* key_cache, const void* value_cache,
+                         int64_t batch, int64_t length, int32_t q_heads, int32_t kv_heads,
+                         int64_t capacity, float scale, void* out, void* stream);
+
+/*
  * Token embedding gather, bit-exact: out[i, :] = table[ids[i], :].
  * Replaces the nn.Embedding call base.embed_tokens(ids) at
  * engine/decode_step.py:38, engine/prefill.py:34, engine/decode.py:19.

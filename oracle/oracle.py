@@ -39,6 +39,8 @@ _SIGNATURES = {
     "or_rope_table": ([_vp, _i32, _vp, _i64, _i64, _vp, _vp], None),
     "or_linear_partials": ([_vp, _i64, _i64, _vp, _i64, _i32, _vp], None),
     "or_linear_silu_mul": ([_vp, _i64, _i64, _vp, _i64, _vp], None),
+    "or_prefill_attention": ([_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i64, ctypes.c_double, _vp,
+                              _vp], None),
     "or_decode_attention": ([_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, ctypes.c_double, _vp, _vp],
                             None),
     "or_lm_head_argmax": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp], None),
@@ -264,6 +266,22 @@ def decode_attention(q, k, v, used, scale: float) -> np.ndarray:
     scratch = np.empty(max(capacity, 1), dtype=np.float64)
     lib().or_decode_attention(_p(q), _p(k), _p(v), _p(used), batch, hq, hk, capacity, float(scale),
                               _p(scratch), _p(out))
+    return out
+
+
+def prefill_attention(q, k, v, length: int, scale: float) -> np.ndarray:
+    """engine/prefill.py:13-23 in float64: causal attention of q bits
+    [B, T, Hq, 128] over the first T slots of k/v bits [B, Hkv, C, 128].
+    Returns bf16 bits [B, T, Hq, 128]."""
+    q, k, v = _u16(q), _u16(k), _u16(v)
+    batch, hq = q.shape[0], q.shape[2]
+    hk, capacity = k.shape[1], k.shape[2]
+    if q.shape[1] != length or length > capacity or hq % hk:
+        raise ValueError("prefill_attention: shapes disagree")
+    out = np.empty_like(q)
+    scratch = np.empty(max(length, 1), dtype=np.float64)
+    lib().or_prefill_attention(_p(q), _p(k), _p(v), batch, length, hq, hk, capacity, float(scale),
+                               _p(scratch), _p(out))
     return out
 
 

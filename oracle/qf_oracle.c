@@ -41,6 +41,11 @@
  *                          head); known answers (zero queries -> mean of V,
  *                          one dominant key block -> its V); wrong head
  *                          mapping and reading past `used` are detected.
+ *   or_prefill_attention   torch float64 scaled_dot_product_attention with
+ *                          is_causal and grouped K/V heads; known answers
+ *                          (zero queries -> running mean of V, a dominant key
+ *                          -> its V from that position on); attending one
+ *                          key past the diagonal is detected.
  *   or_lm_head_argmax      logits bit-equal to torch float64 F.linear rounded
  *                          to bf16; token = torch.argmax of them (first
  *                          maximum) on integer inputs full of exact ties.
@@ -407,6 +412,43 @@ EXPORT void or_decode_attention(const uint16_t* q, const uint16_t* k, const uint
       }
       for (int d = 0; d < HEAD; ++d) o[d] = n ? or_bf16((float)(acc[d] / den)) : 0;
     }
+}
+
+/* Causal prefill attention (engine/prefill.py:13-23, the reference's
+ * aten._flash_attention_forward(..., is_causal=True) over the first `length`
+ * cache slots):
+ *   out[b, t, h] = bf16( softmax_j<=t((q[b,t,h] . k[b,h/G,j]) * scale) @ v[b,h/G,j] )
+ * in double.  q [b, length, hq, 128] (the prefill_qkv layout), k/v
+ * [b, hk, capacity, 128] head-major caches, out like q.  Slots at or beyond
+ * `length` are not read. */
+EXPORT void or_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 int64_t batch, int64_t length, int32_t hq, int32_t hk,
+                                 int64_t capacity, double scale, double* scratch, uint16_t* out) {
+  const int32_t groups = hq / hk;
+  for (int64_t b = 0; b < batch; ++b)
+    for (int64_t t = 0; t < length; ++t)
+      for (int32_t h = 0; h < hq; ++h) {
+        const int64_t vh = b * hk + h / groups;
+        const uint16_t* qr = q + ((b * length + t) * hq + h) * HEAD;
+        uint16_t* o = out + ((b * length + t) * hq + h) * HEAD;
+        double mx = -INFINITY;
+        for (int64_t j = 0; j <= t; ++j) {
+          const uint16_t* kr = k + (vh * capacity + j) * HEAD;
+          double dot = 0.0;
+          for (int d = 0; d < HEAD; ++d) dot += (double)or_f32(qr[d]) * (double)or_f32(kr[d]);
+          scratch[j] = dot * scale;
+          if (scratch[j] > mx) mx = scratch[j];
+        }
+        double acc[HEAD] = {0};
+        double den = 0.0;
+        for (int64_t j = 0; j <= t; ++j) {
+          const double p = exp(scratch[j] - mx);
+          den += p;
+          const uint16_t* vr = v + (vh * capacity + j) * HEAD;
+          for (int d = 0; d < HEAD; ++d) acc[d] += p * (double)or_f32(vr[d]);
+        }
+        for (int d = 0; d < HEAD; ++d) o[d] = or_bf16((float)(acc[d] / den));
+      }
 }
 
 /* ------------------------------------------------ LM head + token choice */

@@ -93,8 +93,6 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b) {
   return s;
 }
 
-__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
-
 // Running softmax state of one lane group for GT query rows; the lane holds
 // the numerator for d = 8r .. 8r+8.
 template <int GT>

@@ -62,6 +62,10 @@ __device__ __forceinline__ void round8(float* f) {
   unpack8(u, f);
 }
 
+// 2^x on the transcendental unit (v_exp_f32); the softmax kernels feed it
+// arguments <= 0.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // Orders one wave's LDS writes before its reads of other lanes' data (and the
 // reads before the next writes); LDS executes a wave's operations in order,
 // so this costs no instruction.

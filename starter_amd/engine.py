@@ -9,8 +9,9 @@ reference runs:
 
 * prefill (``engine/prefill.py:26-66``): embedding gather, RMSNorm, packed QKV
   projection (hipBLASLt), ``prefill_qkv`` (Q/K norm + RoPE + K/V cache write),
-  causal flash attention with grouped K/V heads (torch's fused SDPA kernel, no
-  score matrix in memory), and the residual-add + RMSNorm / SiLU * up fusions;
+  causal flash attention with grouped K/V heads (``prefill_attention``: one
+  launch, no score matrix in memory), and the residual-add + RMSNorm / SiLU *
+  up fusions;
   captured once per (batch, prompt length) in a HIP graph and replayed for
   every prompt of that shape (``engine/prefill.py:65-99``);
 * decode (``engine/decode_step.py:33-64``): the split-K projections whose f32
@@ -43,12 +44,11 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 from torch.nn import functional as F
-from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from .kernels.decode_fused import add_rms_norm, silu_mul
 from .kernels.embedding import embedding
 from .kernels import lm_head as _lm_head
-from .kernels.prefill import prefill_qkv
+from .kernels.prefill import prefill_attention, prefill_qkv
 from .kernels.rmsnorm import rms_norm
 from .kernels.rotary import rope_tables
 from .kernels.skinny_gemm import (linear_partials, linear_partials_merged, linear_silu_mul,
@@ -248,16 +248,11 @@ class Engine:
     # ------------------------------------------------------------ prefill
 
     def _prefill_attention(self, q, keys, values, length):
-        """Causal GQA attention over the prompt: q [B, T, Hq, 128] against the
-        first T cache slots, on torch's fused flash kernel (grouped K/V heads
-        read in place, no score matrix in memory; the math fallback is not
-        allowed).  Returns [B * T, Hq * 128]."""
-        batch = q.shape[0]
-        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
-            out = F.scaled_dot_product_attention(
-                q.transpose(1, 2), keys[:, :, :length], values[:, :, :length],
-                is_causal=True, scale=self.scale, enable_gqa=True)
-        return out.transpose(1, 2).reshape(batch * length, self.q_heads * HEAD)
+        """Causal GQA attention over the prompt, q [B, T, Hq, 128] against the
+        first T cache slots (one flash-attention launch: no score matrix in
+        memory).  Returns [B * T, Hq * 128]."""
+        out = prefill_attention(q, keys, values, length, self.scale)
+        return out.view(q.shape[0] * length, self.q_heads * HEAD)
 
     def _prefill(self, st: _State):
         """Prompt ``st.prompt`` -> K/V cache slots [0, T) of every layer and the

@@ -37,6 +37,7 @@ SIGNATURES = {
                                 _i64, _vp, _vp, _vp, _vp], _i32),
     "qf_prefill_qkv": ([_vp, _i64, _i64, _i32, _i32, _vp, _vp, _f32, _f32, _vp, _vp, _i64, _vp,
                         _vp, _vp, _vp], _i32),
+    "qf_prefill_attention": ([_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i64, _f32, _vp, _vp], _i32),
     "qf_embedding": ([_vp, _i64, _vp, _i64, _i64, _vp, _vp], _i32),
     "qf_rope_table": ([_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp], _i32),
     "qf_linear_splits": ([_i64, _i64, _i64], _i32),

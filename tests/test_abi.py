@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 20
+    assert len(names) == 21
 
 
 def test_library_exports_every_symbol():
@@ -100,6 +100,14 @@ def test_host_side_argument_errors_launch_nothing():
     assert lib.qf_lm_head_argmax(bogus, 1, 2560, bogus, 151930, bogus, bogus, None, None) == -2
     assert lib.qf_lm_head_argmax(bogus, 1, 2560, bogus, 151936, None, bogus, None, None) == -1
     assert lib.qf_lm_head_argmax(bogus + 8, 1, 2560, bogus, 151936, bogus, bogus, None, None) == -3
+    pa = lib.qf_prefill_attention
+    assert pa(bogus, bogus, bogus, 1, 0, 32, 8, 64, 0.1, bogus, None) == -1       # empty prompt
+    assert pa(bogus, bogus, bogus, 1, 65, 32, 8, 64, 0.1, bogus, None) == -1      # past capacity
+    assert pa(None, bogus, bogus, 1, 8, 32, 8, 64, 0.1, bogus, None) == -1
+    assert pa(bogus, bogus, bogus, 1, 8, 32, 8, 64, float("nan"), bogus, None) == -1
+    assert pa(bogus, bogus, bogus, 1, 8, 32, 3, 64, 0.1, bogus, None) == -2       # 32 % 3
+    assert pa(bogus, bogus, bogus, 1, 8, 48, 3, 64, 0.1, bogus, None) == -2       # 16 per kv head
+    assert pa(bogus + 8, bogus, bogus, 1, 8, 32, 8, 64, 0.1, bogus, None) == -3
     # the allocation-free variant checks the same arguments, then its capacity
     # (64 rows x 16,384 blocks fit; one more vocabulary tile does not)
     static = lib.qf_lm_head_argmax_static

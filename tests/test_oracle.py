@@ -550,6 +550,60 @@ def test_decode_attention_known_answers_and_planted_mistakes():
     assert (O.ulp_distance(good, bits(past_end)) > 1).any()
 
 
+# ------------------------------------------------ causal prefill attention
+
+def causal64(q, k, v, length):
+    """torch float64 scaled_dot_product_attention, is_causal, grouped heads:
+    q [B, T, Hq, 128], k/v [B, Hkv, C, 128] -> [B, T, Hq, 128]."""
+    hq, hk = q.shape[2], k.shape[1]
+    kk = k[:, :, :length].double().repeat_interleave(hq // hk, 1)
+    vv = v[:, :, :length].double().repeat_interleave(hq // hk, 1)
+    out = F.scaled_dot_product_attention(q.double().transpose(1, 2), kk, vv, is_causal=True,
+                                         scale=128 ** -0.5)
+    return out.transpose(1, 2)
+
+
+@pytest.mark.parametrize("b,t,hq,hk,cap", [(1, 1, 4, 2, 1), (2, 37, 8, 2, 40), (1, 70, 4, 4, 96),
+                                           (1, 130, 8, 1, 130)])
+def test_prefill_attention_matches_torch_float64(b, t, hq, hk, cap):
+    g = gen(700 + t)
+    q = normal((b, t, hq, 128), g=g)
+    k, v = normal((b, hk, cap, 128), g=g), normal((b, hk, cap, 128), g=g)
+    pk, pv = k.clone(), v.clone()
+    pk[:, :, t:], pv[:, :, t:] = float("nan"), float("nan")   # slots past the prompt
+    got = O.prefill_attention(bits(q), bits(pk), bits(pv), t, 128 ** -0.5)
+    assert not np.isnan(O.bf16_value(got)).any()
+    expected = causal64(q, k, v, t).to(torch.bfloat16)
+    assert_bf16_close(got, expected, max_ulp=1, min_exact=0.999, what="prefill attention")
+
+
+def test_prefill_attention_known_answers_and_planted_mistake():
+    # zero queries: uniform weights over keys 0..t, the running mean of V
+    t = 9
+    q = torch.zeros(1, t, 4, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, t, 128, dtype=torch.bfloat16)
+    v = torch.arange(t, dtype=torch.float32).view(1, 1, t, 1).expand(1, 2, t, 128).to(torch.bfloat16)
+    got = O.bf16_value(O.prefill_attention(bits(q), bits(k), bits(v), t, 128 ** -0.5))
+    for pos in range(t):
+        assert (got[0, pos] == np.float32(pos / 2)).all()       # mean of 0..pos
+    # one dominant key j0: every position from j0 on returns V[j0]
+    q.fill_(8)
+    k.fill_(-8)
+    k[:, :, 4] = 8
+    got = O.bf16_value(O.prefill_attention(bits(q), bits(k), bits(v), t, 128 ** -0.5))
+    assert (got[0, 4:] == 4).all() and (got[0, 3] != 4).all()
+    # planted mistake: attending one key past the diagonal
+    g = gen(720)
+    q, k, v = normal((1, 16, 4, 128), g=g), normal((1, 2, 17, 128), g=g), normal((1, 2, 17, 128), g=g)
+    good = O.prefill_attention(bits(q), bits(k), bits(v), 16, 128 ** -0.5)
+    hq, hk = 4, 2
+    kk, vv = (x[:, :, :17].double().repeat_interleave(hq // hk, 1) for x in (k, v))
+    mask = torch.ones(16, 17, dtype=torch.bool).tril(diagonal=1)
+    shifted = F.scaled_dot_product_attention(q.double().transpose(1, 2), kk, vv, attn_mask=mask,
+                                             scale=128 ** -0.5).transpose(1, 2).to(torch.bfloat16)
+    assert (O.ulp_distance(good, bits(shifted)) > 1).any()
+
+
 # --------------------------------------------------- LM head + token choice
 
 def test_lm_head_argmax_matches_torch_and_breaks_ties_low():
