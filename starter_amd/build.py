@@ -41,6 +41,12 @@ COMPILE_FLAGS = [
     "-Wall",
     "-I", str(ROOT / "include"),
 ]
+# Per-source additions.  Prefill attention rescales its f32 accumulators
+# between matrix-core products; with the accumulators in ordinary VGPRs
+# (instead of AGPRs) no copies are needed between the two register files.
+EXTRA_FLAGS = {
+    "prefill_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def hipcc() -> str:
@@ -70,7 +76,8 @@ def build(verbose: bool = False) -> Path:
     jobs = []
     for name in SOURCES:
         obj = OBJ_DIR / (Path(name).stem + ".o")
-        jobs.append((obj, [cc, *COMPILE_FLAGS, "-c", str(CSRC / name), "-o", str(obj)]))
+        jobs.append((obj, [cc, *COMPILE_FLAGS, *EXTRA_FLAGS.get(name, ()), "-c", str(CSRC / name),
+                           "-o", str(obj)]))
     workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
         for fut in [pool.submit(_run, cmd, verbose) for _, cmd in jobs]:

@@ -43,6 +43,8 @@
 // or NaN cache contents past the prompt never reach a product.
 #include "qf_device.h"
 
+#include <type_traits>
+
 namespace qf {
 namespace {
 
@@ -52,7 +54,6 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
 constexpr int kD = 128;
-constexpr int kQB = 32;                 // query positions per workgroup
 constexpr int kKB = 64;                 // keys per staged block
 constexpr int kKRow = 272;              // LDS bytes per staged K row
 constexpr int kVRow = 288;              // LDS bytes per staged V row
@@ -60,6 +61,10 @@ constexpr int kORow = 272;              // LDS bytes per row of the output stagi
 constexpr int kLoadsPerThread = kKB * kD * 2 / 16 / kBlock;  // 16-byte loads per operand
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kLog2e = 1.4426950408889634f;
+// A row's exponent offset (its reference maximum, log2 units) is raised only
+// when a block's row maximum exceeds it by more than this, so unnormalised
+// probabilities stay below 2^8 and the accumulators are rarely rescaled.
+constexpr float kLazy = 8.0f;
 
 struct PrefillArgs {
   const uint16_t* q;   // [B, T, Hq, 128]
@@ -67,11 +72,21 @@ struct PrefillArgs {
   const uint16_t* v;
   uint16_t* out;       // [B, T, Hq, 128]
   int64_t length, capacity;
-  int32_t q_heads, kv_heads, groups;
-  int32_t qblocks;     // ceil(T / 32)
+  int32_t q_heads, kv_heads;
+  int32_t qblocks;     // ceil(T / query positions per workgroup)
   int32_t pairs;       // B * Hkv
-  float scale_log2;
+  float scale_log2;    // |scale| * log2(e)
+  uint32_t qsign;      // 0x80008000 when scale < 0: Q enters negated (exact in bf16)
 };
+
+// Work split per group size G (query heads per KV head): QB query positions
+// per workgroup (a divisor of the key block, so a workgroup's queries share
+// one diagonal block) and TPW 16-row tiles per wave, G * QB / 16 = 4 TPW.
+template <int G> struct Split;
+template <> struct Split<1> { static constexpr int QB = 64, TPW = 1; };
+template <> struct Split<2> { static constexpr int QB = 32, TPW = 1; };
+template <> struct Split<4> { static constexpr int QB = 32, TPW = 2; };
+template <> struct Split<8> { static constexpr int QB = 16, TPW = 2; };
 
 __device__ __forceinline__ f32x4 mfma32(const uint4& a, const uint4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
@@ -83,11 +98,16 @@ __device__ __forceinline__ v4i16 read_tr(const uint8_t* base, int off) {
       (lds_v4i16*)((__attribute__((address_space(3))) uint8_t*)base + off));
 }
 
-// TPW: 16-row query tiles per wave (the workgroup's 2G tiles over 4 waves).
-template <int TPW>
+template <int G>
 __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t klds[kKB * kKRow];
-  __shared__ __attribute__((aligned(16))) uint8_t vlds[kKB * kVRow];
+  constexpr int QB = Split<G>::QB;
+  constexpr int TPW = Split<G>::TPW;
+  constexpr int kSubs = QB / 16;  // position tiles per head
+  static_assert(G * kSubs == 4 * TPW, "every wave holds TPW tiles");
+  // Two K/V block buffers: block j + 1 is staged into one while block j is
+  // read from the other, so one barrier per block separates the two.
+  __shared__ __attribute__((aligned(16))) uint8_t klds[2][kKB * kKRow];
+  __shared__ __attribute__((aligned(16))) uint8_t vlds[2][kKB * kVRow];
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = tid / kWave;
@@ -99,29 +119,28 @@ __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
   const int pair = (int)(blockIdx.x % a.pairs);
   const int b = pair / a.kv_heads;
   const int kvh = pair % a.kv_heads;
-  const int64_t p0 = (int64_t)qb * kQB;
+  const int64_t p0 = (int64_t)qb * QB;
   const int64_t last = a.length - 1;
   const int nkb = (int)(p0 / kKB) + 1;  // key blocks: all below the diagonal one, and it
   const uint16_t* kbase = a.k + (int64_t)pair * a.capacity * kD;
   const uint16_t* vbase = a.v + (int64_t)pair * a.capacity * kD;
 
-  // This wave's tiles: tile tau = wave + 4u -> head g = tau / 2, positions
-  // p0 + 16 (tau % 2) .. +16 (the same positions for every tile of a wave).
-  const int sub = wave & 1;
-  const int64_t pt = p0 + 16 * sub;
-  const int ntile = 2 * a.groups;
-  bool on[TPW];
+  // This wave's tiles: tile tau = wave + 4u -> head kvh G + tau / kSubs,
+  // positions p0 + 16 (tau % kSubs) .. +16 (the same positions for every
+  // tile of a wave, since kSubs divides 4).
+  const int64_t pt = p0 + 16 * (wave % kSubs);
   int head[TPW];
   uint4 qf[TPW][4];
   const int64_t qpos = pt + r < a.length ? pt + r : last;
 #pragma unroll
   for (int u = 0; u < TPW; ++u) {
-    const int tau = wave + 4 * u;
-    on[u] = tau < ntile;
-    head[u] = kvh * a.groups + (on[u] ? tau / 2 : 0);
+    head[u] = kvh * G + (wave + 4 * u) / kSubs;
     const uint16_t* qr = a.q + (((int64_t)b * a.length + qpos) * a.q_heads + head[u]) * kD;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[u][s] = load16<false>(qr + 8 * g4 + 32 * s);
+    for (int s = 0; s < 4; ++s) {
+      const uint4 x = load16<false>(qr + 8 * g4 + 32 * s);
+      qf[u][s] = make_uint4(x.x ^ a.qsign, x.y ^ a.qsign, x.z ^ a.qsign, x.w ^ a.qsign);
+    }
   }
 
   float mq[TPW], lq[TPW];
@@ -147,69 +166,62 @@ __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
       vreg[i] = load16<true>(vbase + key * kD + 8 * chunk);
     }
   };
-  auto stage = [&]() {
+  auto stage = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
       const int key = tid / 16 + 16 * i;
-      *reinterpret_cast<uint4*>(klds + key * kKRow + 16 * chunk) = kreg[i];
-      *reinterpret_cast<uint4*>(vlds + key * kVRow + 16 * chunk) = vreg[i];
+      *reinterpret_cast<uint4*>(klds[buf] + key * kKRow + 16 * chunk) = kreg[i];
+      *reinterpret_cast<uint4*>(vlds[buf] + key * kVRow + 16 * chunk) = vreg[i];
     }
   };
 
-  const bool any = on[0];  // wave-uniform: a wave without tiles only helps load
   const int vrd = (4 * g4 + (r >> 2)) * kVRow + 8 * (r & 3);
-  fetch(0);
-  for (int j = 0; j < nkb; ++j) {
-    __syncthreads();  // the previous block's LDS reads are done
-    stage();
-    __syncthreads();
-    if (j + 1 < nkb) fetch(j + 1);
-    if (!any) continue;
-    const bool diag = j == nkb - 1;
-    const int64_t key0 = (int64_t)j * kKB;
-    // S^T for the four 16-key tiles of the block, every query tile.
+  // One staged key block against this wave's tiles.  On the diagonal block
+  // (the last) keys past a row's position are masked and 16-key tiles that
+  // start past the wave's last position are skipped; every other block is
+  // entirely visible to every row.
+  auto attend = [&](const uint8_t* kb, const uint8_t* vb, int64_t key0, auto diag_tag) {
+    constexpr bool kDiag = decltype(diag_tag)::value;
+    const int ktn = kDiag ? (int)((pt + 15 - key0) >> 4) + 1 : 4;  // wave-uniform, 1..4
+    // S^T for the attended 16-key tiles of the block, every query tile.
     f32x4 c[TPW][4];
 #pragma unroll
     for (int u = 0; u < TPW; ++u)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) c[u][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < 4; ++kt) {
+      if (kDiag && kt >= ktn) break;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const uint4 kf = *reinterpret_cast<const uint4*>(klds + (16 * kt + r) * kKRow + 16 * (g4 + 4 * s));
+        const uint4 kf = *reinterpret_cast<const uint4*>(kb + (16 * kt + r) * kKRow + 16 * (g4 + 4 * s));
 #pragma unroll
         for (int u = 0; u < TPW; ++u) c[u][kt] = mfma32(kf, qf[u][s], c[u][kt]);
       }
+    }
     uint4 pa[TPW][2];
 #pragma unroll
     for (int u = 0; u < TPW; ++u) {
-      // Lane: query pt + r, keys key0 + 16 kt + 4 g4 + i.
-      float sc[4][4], bm = kNegInf;
+      // Lane: query pt + r, keys key0 + 16 kt + 4 g4 + i (raw dot products).
+      bool live[4][4];
+      float bm = kNegInf;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const bool live = !diag || key0 + 16 * kt + 4 * g4 + i <= pt + r;
-          sc[kt][i] = live ? c[u][kt][i] * a.scale_log2 : kNegInf;
-          bm = fmaxf(bm, sc[kt][i]);
+          live[kt][i] = !kDiag || key0 + 16 * kt + 4 * g4 + i <= pt + r;
+          bm = fmaxf(bm, live[kt][i] ? c[u][kt][i] : kNegInf);
         }
       bm = fmaxf(bm, __shfl_xor(bm, 16));
       bm = fmaxf(bm, __shfl_xor(bm, 32));
-      const float mn = fmaxf(mq[u], bm);
-      const float corr = mn == kNegInf ? 1.0f : exp2_hw(mq[u] - mn);
-      float p[4][4], ps = 0.0f;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[kt][i] = mn == kNegInf ? 0.0f : exp2_hw(sc[kt][i] - mn);
-          ps += p[kt][i];
-        }
-      lq[u] = lq[u] * corr + ps;
-      mq[u] = mn;
-      // O row 4 g4 + i belongs to query 4 g4 + i, whose factor lane 4 g4 + i holds.
-      if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0) {  // wave-uniform
+      bm *= a.scale_log2;  // the row's scaled maximum (rounding is monotonic)
+      if (__builtin_amdgcn_ballot_w64(bm > mq[u] + kLazy) != 0) {  // wave-uniform
+        // Raise the offsets to the block maxima; O row 4 g4 + i belongs to
+        // query 4 g4 + i, whose factor lane 4 g4 + i holds.
+        const float mn = fmaxf(mq[u], bm);
+        const float corr = exp2_hw(mq[u] - mn);
+        lq[u] *= corr;
+        mq[u] = mn;
         float cr[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) cr[i] = __shfl(corr, 4 * g4 + i);
@@ -218,6 +230,16 @@ __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) o[u][db][i] *= cr[i];
       }
+      const float nm = -mq[u];
+      float p[4][4], ps = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[kt][i] = live[kt][i] ? exp2_hw(fmaf(c[u][kt][i], a.scale_log2, nm)) : 0.0f;
+          ps += p[kt][i];
+        }
+      lq[u] += ps;
       // The probabilities, rounded to bf16, as the A operand of the two k steps.
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
@@ -225,26 +247,41 @@ __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
                                pack2(p[2 * ks + 1][0], p[2 * ks + 1][1]),
                                pack2(p[2 * ks + 1][2], p[2 * ks + 1][3]));
     }
+    const int ksn = ktn > 2 ? 2 : 1;  // 32-key steps with an attended tile
 #pragma unroll
     for (int db = 0; db < 8; ++db)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const v4i16 lo = read_tr(vlds, vrd + 32 * ks * kVRow + 32 * db);
-        const v4i16 hi = read_tr(vlds, vrd + (32 * ks + 16) * kVRow + 32 * db);
-        const uint4 vb = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
+        if (kDiag && ks >= ksn) break;
+        const v4i16 lo = read_tr(vb, vrd + 32 * ks * kVRow + 32 * db);
+        const v4i16 hi = read_tr(vb, vrd + (32 * ks + 16) * kVRow + 32 * db);
+        const uint4 vt = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
                                     __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
 #pragma unroll
-        for (int u = 0; u < TPW; ++u) o[u][db] = mfma32(pa[u][ks], vb, o[u][db]);
+        for (int u = 0; u < TPW; ++u) o[u][db] = mfma32(pa[u][ks], vt, o[u][db]);
       }
+  };
+
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  for (int j = 0; j + 1 < nkb; ++j) {
+    // Block j is in buffer j % 2; block j + 1's loads fly during its
+    // arithmetic and land in the other buffer, last read during block j - 1
+    // (before the previous barrier).
+    fetch(j + 1);
+    attend(klds[j & 1], vlds[j & 1], (int64_t)j * kKB, std::false_type{});
+    stage((j + 1) & 1);
+    __syncthreads();
   }
+  attend(klds[(nkb - 1) & 1], vlds[(nkb - 1) & 1], (int64_t)(nkb - 1) * kKB, std::true_type{});
 
   // O / l in bf16, through LDS (this wave's 16 x 128 tile, one tile at a
   // time) so that every lane stores 16 contiguous bytes of one output row.
   __syncthreads();  // every wave is done with the K/V blocks
-  uint8_t* ot = klds + wave * 16 * kORow;
+  uint8_t* ot = klds[0] + wave * 16 * kORow;
 #pragma unroll
   for (int u = 0; u < TPW; ++u) {
-    if (!on[u]) break;  // wave-uniform
     float lt = lq[u] + __shfl_xor(lq[u], 16);
     lt += __shfl_xor(lt, 32);  // lanes of query r: its denominator
     float inv[4];
@@ -272,10 +309,13 @@ __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
   }
 }
 
-template <int TPW>
-int launch_prefill(const PrefillArgs& a, hipStream_t s) {
+template <int G>
+int launch_prefill(PrefillArgs a, hipStream_t s) {
+  constexpr int QB = Split<G>::QB;
+  a.qblocks = (int32_t)((a.length + QB - 1) / QB);
   const int64_t blocks = (int64_t)a.qblocks * a.pairs;
-  hipLaunchKernelGGL((prefill_attn_kernel<TPW>), dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
+  if (blocks > (int64_t)INT32_MAX) return QF_E_SHAPE;
+  hipLaunchKernelGGL((prefill_attn_kernel<G>), dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
   return launch_status();
 }
 
@@ -305,17 +345,16 @@ extern "C" int qf_prefill_attention(const void* q, const void* key_cache, const 
   a.capacity = capacity;
   a.q_heads = q_heads;
   a.kv_heads = kv_heads;
-  a.groups = groups;
-  a.qblocks = (int32_t)((length + kQB - 1) / kQB);
+  if (batch * kv_heads > INT32_MAX) return QF_E_SHAPE;
+  a.qblocks = 0;
   a.pairs = (int32_t)(batch * kv_heads);
-  a.scale_log2 = scale * kLog2e;
-  if ((int64_t)a.qblocks * a.pairs > (int64_t)INT32_MAX || batch * kv_heads > INT32_MAX)
-    return QF_E_SHAPE;
+  a.scale_log2 = (scale < 0.0f ? -scale : scale) * kLog2e;
+  a.qsign = scale < 0.0f ? 0x80008000u : 0u;
   hipStream_t s = as_stream(stream);
   switch (groups) {
-    case 1:
-    case 2: return launch_prefill<1>(a, s);
-    case 4: return launch_prefill<2>(a, s);
-    default: return launch_prefill<4>(a, s);
+    case 1: return launch_prefill<1>(a, s);
+    case 2: return launch_prefill<2>(a, s);
+    case 4: return launch_prefill<4>(a, s);
+    default: return launch_prefill<8>(a, s);
   }
 }

@@ -10,7 +10,11 @@ Shapes cover 1, 2, 4 and 8 query heads per KV head, prompts that end inside a
 query block and inside a key block, one token, and the Qwen3-4B head layout;
 cache slots past the prompt hold NaN and must never reach the output.  Known
 answers: zero queries give the running mean of V exactly; inputs stay
-untouched; a captured graph replays with new contents.
+untouched; a captured graph replays with new contents.  Scores that climb
+across key blocks (every block raises the row maxima by more than the lazy
+rescale threshold) and that fall (no block after the first raises them), and
+negative and zero scales (Q enters negated, exact in bf16), cover the
+rescaling branches.
 """
 
 from __future__ import annotations
@@ -39,8 +43,8 @@ def operands(b, t, hq, hk, cap, seed, poison=True):
     return q, k, v
 
 
-def check(got, q, k, v, t, what):
-    want = O.bf16_value(O.prefill_attention(bits(q), bits(k), bits(v), t, SCALE))
+def check(got, q, k, v, t, what, scale=SCALE):
+    want = O.bf16_value(O.prefill_attention(bits(q), bits(k), bits(v), t, scale))
     have = O.bf16_value(bits(got))
     assert not np.isnan(have).any(), f"{what}: NaN in the output"
     np.testing.assert_allclose(have, want, rtol=0.02, atol=0.004, err_msg=what)
@@ -67,6 +71,29 @@ def test_matches_oracle(b, t, hq, hk, cap):
     check(out, q, k, v, t, f"b{b} t{t} hq{hq} hk{hk}")
     for before, after in zip(snapshot, (qd, kd, vd)):   # inputs untouched
         assert torch.equal(before.view(torch.int16), after.view(torch.int16))
+
+
+@pytest.mark.parametrize("scale", [-SCALE, 0.0, 3 * SCALE])
+def test_other_scales(scale):
+    b, t, hq, hk, cap = 2, 150, 8, 2, 160
+    q, k, v = operands(b, t, hq, hk, cap, 860)
+    out = prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV), t, scale)
+    check(out, q, k, v, t, f"scale {scale}", scale)
+
+
+@pytest.mark.parametrize("climb", [True, False])
+def test_monotone_scores(climb):
+    """Key j = c_j (1, .., 1), q = 1/4: the score of key j is 2 c_j, exact.
+    Climbing c_j = j / 16 lifts every row maximum by ~16 (log2 units) per
+    block, past the rescale threshold; falling c_j puts the maximum at key 0."""
+    b, t, hq, hk = 1, 250, 8, 2
+    j = torch.arange(t, dtype=torch.float32)
+    c = j / 16 if climb else (t - 1 - j) / 16
+    k = c.view(1, 1, t, 1).expand(b, hk, t, 128).to(torch.bfloat16).contiguous()
+    q = torch.full((b, t, hq, 128), 0.25).to(torch.bfloat16)
+    v = normal((b, hk, t, 128), g=gen(861))
+    out = prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV), t, SCALE)
+    check(out, q, k, v, t, f"climb={climb}")
 
 
 def test_zero_queries_give_the_running_mean():
