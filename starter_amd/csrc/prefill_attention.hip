@@ -84,7 +84,7 @@ struct PrefillArgs {
 // one diagonal block) and TPW 16-row tiles per wave, G * QB / 16 = 4 TPW.
 template <int G> struct Split;
 template <> struct Split<1> { static constexpr int QB = 64, TPW = 1; };
-template <> struct Split<2> { static constexpr int QB = 32, TPW = 1; };
+template <> struct Split<2> { static constexpr int QB = 64, TPW = 2; };
 template <> struct Split<4> { static constexpr int QB = 32, TPW = 2; };
 template <> struct Split<8> { static constexpr int QB = 16, TPW = 2; };
 
