@@ -244,6 +244,41 @@ int qf_linear_silu_mul(const void* x, int64_t rows, int64_t k, const void* gate_
                        int64_t n, void* out, void* stream);
 
 /*
+ * Decode projections at 1..4 rows as QF_ROW_GROUPS workgroups (one per
+ * compute unit), each over the whole K range of n / QF_ROW_GROUPS columns,
+ * so that the residual add and the RMSNorm of the decode step's add + norm
+ * launch move into the projections on either side of it.  They replace the
+ * down projection + add + norm of engine/decode_step.py:56-59,
+ * linear_partials (engine/kernels/skinny_gemm.py:100-109) then add_rms_norm
+ * (engine/kernels/decode_fused.py:140-160), and the next layer's qkv
+ * projection of the normalised row (engine/decode_step.py:43-44).
+ *
+ * Shapes: x / total bf16 [rows, k], weight bf16 [n, k], all contiguous and
+ * 16-byte aligned; k % 8 == 0; n = QF_ROW_GROUPS * c with
+ * c in {2, 4, 8, 10, 16, 24, 32} and (rows <= 2 ? rows : 4) * c <= 32;
+ * qf_row_supported answers for a shape, others get QF_E_SHAPE.  sq is
+ * f64 [rows, QF_ROW_GROUPS], 8-byte aligned.
+ *
+ * qf_linear_rows:     out = bf16(x W^T)  (f32 accumulation).
+ * qf_linear_residual: y = bf16(x W^T);  total = bf16(residual + y) (total
+ *                     may alias residual) and sq[r][g] = the f64 sum of
+ *                     total[r][j]^2 over workgroup g's columns j.
+ * qf_linear_normed:   x = bf16(bf16(total * inv) * gain) with
+ *                     inv = 1 / sqrt(f32(sum_g sq[r][g]) / k + eps), the
+ *                     rounding steps of qf_add_rms_norm (so x equals the row
+ *                     it would write); out = bf16(x W^T).
+ */
+#define QF_ROW_GROUPS 256
+int qf_row_supported(int32_t rows, int64_t k, int64_t n);
+int qf_linear_rows(const void* x, int32_t rows, int64_t k, const void* weight, int64_t n,
+                   void* out, void* stream);
+int qf_linear_residual(const void* x, int32_t rows, int64_t k, const void* weight, int64_t n,
+                       const void* residual, void* total, double* sq, void* stream);
+int qf_linear_normed(const void* total, const double* sq, const void* gain, float eps,
+                     int32_t rows, int64_t k, const void* weight, int64_t n, void* out,
+                     void* stream);
+
+/*
  * Key-segment plan of qf_decode_attention for virtual_heads = batch * Hkv
  * heads of a cache with `capacity` slots on a GPU with compute_units CUs:
  * at most one workgroup per CU, segments of whole 64-key tiles, at most 32.

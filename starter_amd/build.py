@@ -28,7 +28,7 @@ CSRC = PACKAGE / "csrc"
 OBJ_DIR = PACKAGE / "_build"
 LIBRARY = PACKAGE / "kernels" / "libqwen_fused.so"
 SOURCES = ("rmsnorm.hip", "silu_mul.hip", "qk_norm_rope.hip", "embedding.hip", "skinny_gemm.hip",
-           "decode_attention.hip", "prefill_attention.hip")
+           "decode_attention.hip", "prefill_attention.hip", "row_gemv.hip")
 ARCH = "gfx950"
 
 COMPILE_FLAGS = [

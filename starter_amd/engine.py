@@ -19,9 +19,13 @@ reference runs:
   also does ``qkv_norm_rope_cache``'s Q/K norm, RoPE and cache write in its
   own launches; at small batches the o_proj projection merges the attention's
   key segments itself), the fused gate/up projection with its SiLU epilogue, and
-  the LM head fused with the greedy token choice; the whole step is captured once per
-  (batch, capacity) in a HIP graph and replayed with the position and cache
-  lengths advanced on the device.
+  the LM head fused with the greedy token choice; at one to four sequences the
+  down projection and the next layer's qkv projection run one workgroup per
+  compute unit over the whole K range, with the residual add in the first
+  one's epilogue and the next RMSNorm in the second one's prologue (one
+  launch fewer per layer, bit-identical normalised rows); the whole step is
+  captured once per (batch, capacity) in a HIP graph and replayed with the
+  position and cache lengths advanced on the device.
 
 Tokens reach the host as ``engine/decode.py:110-128`` moves them: step k's
 device-to-host copy into pinned memory is queued before step k + 1 is
@@ -51,6 +55,7 @@ from .kernels import lm_head as _lm_head
 from .kernels.prefill import prefill_attention, prefill_qkv
 from .kernels.rmsnorm import rms_norm
 from .kernels.rotary import rope_tables
+from .kernels import row_gemv
 from .kernels.skinny_gemm import (linear_partials, linear_partials_merged, linear_silu_mul,
                                   supports, supports_merged)
 from .kernels.small_query_attention import SmallQueryAttention
@@ -143,6 +148,14 @@ class _State:
         self.merged_o = (batch <= MERGED_O_BATCH and self.attention.splits > 1
                          and supports_merged(self.attention.partials, self.attention.stats, batch,
                                              engine.layers[0].o))
+        # Down projection with the residual add, next qkv projection with the
+        # RMSNorm (no add + norm launch between them) where the shapes allow.
+        first = engine.layers[0]
+        self.fold_norms = (engine.fold_norms and len(engine.layers) > 1
+                           and row_gemv.supports_shape(batch, first.down.shape[1],
+                                                       first.down.shape[0])
+                           and row_gemv.supports_shape(batch, first.qkv.shape[1],
+                                                       first.qkv.shape[0]))
         self.prompt = torch.zeros((batch, length), dtype=torch.int64, device=dev)
         self.tokens = torch.zeros(batch, dtype=torch.int64, device=dev)
         self.position = torch.zeros(1, dtype=torch.int64, device=dev)
@@ -163,9 +176,11 @@ class Engine:
 
     def __init__(self, model_path: str | None = None, *, config=None, seed: int = 0,
                  device: str | torch.device = "cuda", use_graphs: bool = True,
-                 keep_logits: bool = False):
+                 keep_logits: bool = False, fold_norms: bool = True):
         """``keep_logits``: also keep each step's bf16 logits in ``last_logits``
-        (a device copy per step; for tests and inspection)."""
+        (a device copy per step; for tests and inspection).  ``fold_norms``:
+        at 1-4 sequences fold the add + norm after the down projection into
+        the projections around it (off: the split-K path at every batch)."""
         from transformers import Qwen3ForCausalLM
         self.device = torch.device(device)
         if self.device.type != "cuda" or not torch.cuda.is_available():
@@ -198,6 +213,7 @@ class Engine:
         self.inv_freq = model.model.rotary_emb.inv_freq.float()
         self.use_graphs = use_graphs
         self.keep_logits = keep_logits
+        self.fold_norms = fold_norms
         self.state: _State | None = None
         self.last_logits = None
         # One side stream for every warm-up and capture: torch keeps a BLAS
@@ -307,9 +323,15 @@ class Engine:
         x = embedding(st.tokens, self.embed)
         first = self.layers[0]
         normed = rms_norm(x, first.ln_in, first.eps_in)
+        sq = None  # set while x's RMSNorm is left to the next qkv projection
+        last = len(self.layers) - 1
         for index, layer in enumerate(self.layers):
+            if sq is None:
+                qkv = self._project(normed, layer.qkv)
+            else:
+                qkv = row_gemv.linear_normed(x, sq, layer.ln_in, layer.eps_in, layer.qkv)
             # qkv_norm_rope_cache + attention, fused into the attention launches
-            args = (self._project(normed, layer.qkv), layer.q_norm, layer.k_norm, layer.eps_q,
+            args = (qkv, layer.q_norm, layer.k_norm, layer.eps_q,
                     layer.eps_k, st.cos, st.sin, st.position, st.keys[index], st.values[index],
                     st.used, self.scale)
             if st.merged_o:
@@ -319,8 +341,12 @@ class Engine:
                 o = self._project(st.attention.run_qkv(*args).view(batch, -1), layer.o)
             x, normed = add_rms_norm(x, o, layer.ln_post, layer.eps_post)
             hidden = self._mlp_hidden(normed, layer.gate_up)
-            weight, eps = self._next_norm(index)
-            x, normed = add_rms_norm(x, self._project(hidden, layer.down), weight, eps)
+            if st.fold_norms and index < last:
+                x, sq = row_gemv.linear_residual(hidden, layer.down, x)
+            else:
+                weight, eps = self._next_norm(index)
+                x, normed = add_rms_norm(x, self._project(hidden, layer.down), weight, eps)
+                sq = None
         logits = self._select(normed, st.tokens)
         st.position.add_(1)
         st.used.add_(1)

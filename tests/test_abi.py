@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 21
+    assert len(names) == 25
 
 
 def test_library_exports_every_symbol():
@@ -149,6 +149,28 @@ def test_host_side_argument_errors_launch_nothing():
                  1, 8, 2, 64, 0.1, 1, 64, None, None, bogus, None) == -3   # misaligned position
     assert fused(bogus + 2, 0, bogus, bogus, 1e-6, 1e-6, bogus, bogus, bogus, bogus, bogus, bogus,
                  1, 8, 2, 64, 0.1, 1, 64, None, None, bogus, None) == -3
+    # one-workgroup-per-CU projections: rows 1..4, N = 256 c for the served c
+    # (padded rows x c <= 32), K % 8; then pointers, eps, alignment
+    assert lib.qf_row_supported(1, 9728, 2560) == 1 and lib.qf_row_supported(1, 2560, 6144) == 1
+    assert lib.qf_row_supported(2, 2560, 4096) == 1 and lib.qf_row_supported(4, 64, 2048) == 1
+    assert lib.qf_row_supported(5, 2560, 2560) == 0 and lib.qf_row_supported(0, 2560, 2560) == 0
+    assert lib.qf_row_supported(3, 2560, 2560) == 0       # padded to 4 rows x 10 columns
+    assert lib.qf_row_supported(1, 2560, 2560 + 256) == 0  # 11 columns per workgroup
+    assert lib.qf_row_supported(1, 2564, 2560) == 0 and lib.qf_row_supported(1, 2560, 128) == 0
+    rows = lib.qf_linear_rows
+    assert rows(bogus, 5, 2560, bogus, 2560, bogus, None) == -2
+    assert rows(None, 1, 2560, bogus, 2560, bogus, None) == -1
+    assert rows(bogus + 8, 1, 2560, bogus, 2560, bogus, None) == -3
+    res = lib.qf_linear_residual
+    assert res(bogus, 1, 9728, bogus, 2560 + 256, bogus, bogus, bogus, None) == -2
+    assert res(bogus, 1, 9728, bogus, 2560, bogus, bogus, None, None) == -1
+    assert res(bogus, 1, 9728, bogus, 2560, bogus, bogus, bogus + 4, None) == -3
+    nrm = lib.qf_linear_normed
+    assert nrm(bogus, bogus, bogus, 1e-6, 1, 2560, bogus, 6144 + 256, bogus, None) == -2
+    assert nrm(bogus, None, bogus, 1e-6, 1, 2560, bogus, 6144, bogus, None) == -1
+    assert nrm(bogus, bogus, bogus, float("nan"), 1, 2560, bogus, 6144, bogus, None) == -1
+    assert nrm(bogus, bogus, bogus, -1.0, 1, 2560, bogus, 6144, bogus, None) == -1
+    assert nrm(bogus, bogus, bogus + 8, 1e-6, 1, 2560, bogus, 6144, bogus, None) == -3
 
 
 def test_empty_inputs_are_no_ops():
