@@ -255,7 +255,7 @@ int qf_linear_silu_mul(const void* x, int64_t rows, int64_t k, const void* gate_
  *
  * Shapes: x / total bf16 [rows, k], weight bf16 [n, k], all contiguous and
  * 16-byte aligned; k % 8 == 0; n = QF_ROW_GROUPS * c with
- * c in {2, 4, 8, 10, 16, 24, 32} and (rows <= 2 ? rows : 4) * c <= 32;
+ * c in {2, 4, 8, 10, 16, 24, 32} and (rows <= 2 ? rows : 4) * c <= 128;
  * qf_row_supported answers for a shape, others get QF_E_SHAPE.  sq is
  * f64 [rows, QF_ROW_GROUPS], 8-byte aligned.
  *
@@ -277,6 +277,39 @@ int qf_linear_residual(const void* x, int32_t rows, int64_t k, const void* weigh
 int qf_linear_normed(const void* total, const double* sq, const void* gain, float eps,
                      int32_t rows, int64_t k, const void* weight, int64_t n, void* out,
                      void* stream);
+
+/*
+ * The other half of a decoder layer in the same form: the attention's output
+ * projection with the residual add (replacing engine/decode_step.py:48-52,
+ * o_proj then add_rms_norm), and the gate/up projection of the normalised
+ * row with the SiLU * up epilogue (engine/decode_step.py:53,
+ * linear_silu_mul of add_rms_norm's output; engine/kernels/skinny_gemm.py:
+ * 112-121).
+ *
+ * qf_linear_residual_merged: x = the merge of the decode attention's key
+ *   segments, exactly as qf_linear_partials_merged takes them (seg_partials
+ *   f32 [rows * kv_heads, segments, G, 128], seg_stats f32
+ *   [rows * kv_heads, segments, 2, G], 2 <= segments <= 32; the bits of the
+ *   attention's own merge), k = q_heads * 128; then as qf_linear_residual.
+ *   qf_row_merged_supported answers for a shape (the merged rows are staged
+ *   in LDS: (rows <= 2 ? rows : 4) * k <= 32768).
+ * qf_linear_silu_mul_normed: x = the normalised row as qf_linear_normed;
+ *   g = bf16(x @ gate^T), u = bf16(x @ up^T) for the packed gate_up bf16
+ *   [2n, k] (gate rows first); out bf16 [rows, n] =
+ *   bf16(float(bf16(silu(g))) * float(u)), the SiLU of qf_linear_silu_mul.
+ *   2n = QF_ROW_GROUPS * c with c in {4, 8, 16, 32, 76} and
+ *   (rows <= 2 ? rows : 4) * c <= 128 (qf_row_silu_supported).
+ */
+int qf_row_merged_supported(int32_t rows, int32_t segments, int32_t q_heads, int32_t kv_heads,
+                            int64_t n);
+int qf_linear_residual_merged(const float* seg_partials, const float* seg_stats,
+                              int32_t segments, int32_t rows, int32_t q_heads, int32_t kv_heads,
+                              const void* weight, int64_t n, const void* residual, void* total,
+                              double* sq, void* stream);
+int qf_row_silu_supported(int32_t rows, int64_t k, int64_t n);
+int qf_linear_silu_mul_normed(const void* total, const double* sq, const void* gain, float eps,
+                              int32_t rows, int64_t k, const void* gate_up, int64_t n, void* out,
+                              void* stream);
 
 /*
  * Key-segment plan of qf_decode_attention for virtual_heads = batch * Hkv

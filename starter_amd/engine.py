@@ -19,11 +19,12 @@ reference runs:
   also does ``qkv_norm_rope_cache``'s Q/K norm, RoPE and cache write in its
   own launches; at small batches the o_proj projection merges the attention's
   key segments itself), the fused gate/up projection with its SiLU epilogue, and
-  the LM head fused with the greedy token choice; at one to four sequences the
-  down projection and the next layer's qkv projection run one workgroup per
-  compute unit over the whole K range, with the residual add in the first
-  one's epilogue and the next RMSNorm in the second one's prologue (one
-  launch fewer per layer, bit-identical normalised rows); the whole step is
+  the LM head fused with the greedy token choice; at batch 1 the
+  projections run one workgroup per compute unit over the whole K range,
+  so both residual adds move into the epilogues of o_proj (which also merges
+  the attention's key segments) and down, and both RMSNorms into the
+  prologues of gate/up and the next qkv projection (two launches fewer per
+  layer, bit-identical normalised rows); the whole step is
   captured once per (batch, capacity) in a HIP graph and replayed with the
   position and cache lengths advanced on the device.
 
@@ -127,6 +128,15 @@ def check_rotary(model) -> None:
 
 #: Largest batch whose decode step merges attention segments inside o_proj.
 MERGED_O_BATCH = 1
+#: Largest batch whose decode step folds the add + norm launches into the
+#: one-workgroup-per-CU projections (measured: batch 1 1,989 against 2,121
+#: us/step with the down/qkv fold alone and ~2,190 with neither; at batch 4
+#: the 4-row projections lose to the split-K ones, 2,434 against 2,396).
+FOLD_BATCH = 1
+#: Whether the folded path merges the attention's segments inside o_proj
+#: (every workgroup merges every head: 2,154 us/step at batch 1) instead of
+#: taking the attention's own merge launch (1,989 us/step).
+MERGE_IN_O_PROJ = False
 
 
 class _State:
@@ -151,11 +161,20 @@ class _State:
         # Down projection with the residual add, next qkv projection with the
         # RMSNorm (no add + norm launch between them) where the shapes allow.
         first = engine.layers[0]
-        self.fold_norms = (engine.fold_norms and len(engine.layers) > 1
+        self.fold_norms = (engine.fold_norms and batch <= FOLD_BATCH and len(engine.layers) > 1
                            and row_gemv.supports_shape(batch, first.down.shape[1],
                                                        first.down.shape[0])
                            and row_gemv.supports_shape(batch, first.qkv.shape[1],
                                                        first.qkv.shape[0]))
+        # o_proj with the residual add (merging the attention's segments),
+        # gate/up with the RMSNorm: the add + norm after the attention.
+        hidden, inner = first.o.shape[0], first.down.shape[1]
+        splits = self.attention.splits
+        o_ok = (row_gemv.supports_merged_shape(batch, splits, engine.q_heads, engine.kv_heads,
+                                               hidden) if MERGE_IN_O_PROJ and splits > 1 else
+                row_gemv.supports_shape(batch, first.o.shape[1], hidden))
+        self.fold_attention = (engine.fold_norms and batch <= FOLD_BATCH and o_ok
+                               and row_gemv.supports_silu_shape(batch, hidden, inner))
         self.prompt = torch.zeros((batch, length), dtype=torch.int64, device=dev)
         self.tokens = torch.zeros(batch, dtype=torch.int64, device=dev)
         self.position = torch.zeros(1, dtype=torch.int64, device=dev)
@@ -179,8 +198,9 @@ class Engine:
                  keep_logits: bool = False, fold_norms: bool = True):
         """``keep_logits``: also keep each step's bf16 logits in ``last_logits``
         (a device copy per step; for tests and inspection).  ``fold_norms``:
-        at 1-4 sequences fold the add + norm after the down projection into
-        the projections around it (off: the split-K path at every batch)."""
+        up to FOLD_BATCH sequences fold both add + norm launches of a layer
+        into the projections around them (off: the split-K path at every
+        batch)."""
         from transformers import Qwen3ForCausalLM
         self.device = torch.device(device)
         if self.device.type != "cuda" or not torch.cuda.is_available():
@@ -334,13 +354,25 @@ class Engine:
             args = (qkv, layer.q_norm, layer.k_norm, layer.eps_q,
                     layer.eps_k, st.cos, st.sin, st.position, st.keys[index], st.values[index],
                     st.used, self.scale)
-            if st.merged_o:
-                st.attention.run_qkv_unmerged(*args)
-                o = linear_partials_merged(st.attention.partials, st.attention.stats, batch, layer.o)
+            if st.fold_attention:
+                if MERGE_IN_O_PROJ and st.attention.splits > 1:
+                    st.attention.run_qkv_unmerged(*args)
+                    x, sq = row_gemv.linear_residual_merged(st.attention.partials,
+                                                            st.attention.stats, batch, layer.o, x)
+                else:
+                    attended = st.attention.run_qkv(*args).view(batch, -1)
+                    x, sq = row_gemv.linear_residual(attended, layer.o, x)
+                hidden = row_gemv.linear_silu_mul_normed(x, sq, layer.ln_post, layer.eps_post,
+                                                         layer.gate_up)
             else:
-                o = self._project(st.attention.run_qkv(*args).view(batch, -1), layer.o)
-            x, normed = add_rms_norm(x, o, layer.ln_post, layer.eps_post)
-            hidden = self._mlp_hidden(normed, layer.gate_up)
+                if st.merged_o:
+                    st.attention.run_qkv_unmerged(*args)
+                    o = linear_partials_merged(st.attention.partials, st.attention.stats, batch,
+                                               layer.o)
+                else:
+                    o = self._project(st.attention.run_qkv(*args).view(batch, -1), layer.o)
+                x, normed = add_rms_norm(x, o, layer.ln_post, layer.eps_post)
+                hidden = self._mlp_hidden(normed, layer.gate_up)
             if st.fold_norms and index < last:
                 x, sq = row_gemv.linear_residual(hidden, layer.down, x)
             else:

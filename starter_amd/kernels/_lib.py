@@ -49,6 +49,11 @@ SIGNATURES = {
     "qf_linear_rows": ([_vp, _i32, _i64, _vp, _i64, _vp, _vp], _i32),
     "qf_linear_residual": ([_vp, _i32, _i64, _vp, _i64, _vp, _vp, _vp, _vp], _i32),
     "qf_linear_normed": ([_vp, _vp, _vp, _f32, _i32, _i64, _vp, _i64, _vp, _vp], _i32),
+    "qf_row_merged_supported": ([_i32, _i32, _i32, _i32, _i64], _i32),
+    "qf_linear_residual_merged": ([_vp, _vp, _i32, _i32, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _vp],
+                                  _i32),
+    "qf_row_silu_supported": ([_i32, _i64, _i64], _i32),
+    "qf_linear_silu_mul_normed": ([_vp, _vp, _vp, _f32, _i32, _i64, _vp, _i64, _vp, _vp], _i32),
     "qf_attention_partition": ([_i64, _i64, _i32, _vp, _vp], _i32),
     "qf_decode_attention": ([_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _f32, _i32, _i64, _vp, _vp,
                              _vp, _vp], _i32),

@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 25
+    assert len(names) == 29
 
 
 def test_library_exports_every_symbol():
@@ -154,7 +154,8 @@ def test_host_side_argument_errors_launch_nothing():
     assert lib.qf_row_supported(1, 9728, 2560) == 1 and lib.qf_row_supported(1, 2560, 6144) == 1
     assert lib.qf_row_supported(2, 2560, 4096) == 1 and lib.qf_row_supported(4, 64, 2048) == 1
     assert lib.qf_row_supported(5, 2560, 2560) == 0 and lib.qf_row_supported(0, 2560, 2560) == 0
-    assert lib.qf_row_supported(3, 2560, 2560) == 0       # padded to 4 rows x 10 columns
+    assert lib.qf_row_supported(3, 2560, 2560) == 1       # padded to 4 rows x 10 columns
+    assert lib.qf_row_supported(4, 2560, 8192) == 1 and lib.qf_row_supported(1, 2560, 256 * 76) == 0
     assert lib.qf_row_supported(1, 2560, 2560 + 256) == 0  # 11 columns per workgroup
     assert lib.qf_row_supported(1, 2564, 2560) == 0 and lib.qf_row_supported(1, 2560, 128) == 0
     rows = lib.qf_linear_rows
@@ -171,6 +172,23 @@ def test_host_side_argument_errors_launch_nothing():
     assert nrm(bogus, bogus, bogus, float("nan"), 1, 2560, bogus, 6144, bogus, None) == -1
     assert nrm(bogus, bogus, bogus, -1.0, 1, 2560, bogus, 6144, bogus, None) == -1
     assert nrm(bogus, bogus, bogus + 8, 1e-6, 1, 2560, bogus, 6144, bogus, None) == -3
+    # gate/up with the norm and SiLU * up: 2n = 256 c, c in 4, 8, 16, 32, 76
+    assert lib.qf_row_silu_supported(1, 2560, 9728) == 1 and lib.qf_row_silu_supported(2, 2560, 9728) == 0
+    assert lib.qf_row_silu_supported(4, 256, 512) == 1 and lib.qf_row_silu_supported(1, 256, 640) == 0
+    silu = lib.qf_linear_silu_mul_normed
+    assert silu(bogus, bogus, bogus, 1e-6, 2, 2560, bogus, 9728, bogus, None) == -2
+    assert silu(bogus, None, bogus, 1e-6, 1, 2560, bogus, 9728, bogus, None) == -1
+    assert silu(bogus, bogus, bogus, float("inf"), 1, 2560, bogus, 9728, bogus, None) == -1
+    assert silu(bogus, bogus + 4, bogus, 1e-6, 1, 2560, bogus, 9728, bogus, None) == -3
+    # o_proj over the attention segments with the residual add
+    assert lib.qf_row_merged_supported(1, 9, 32, 8, 2560) == 1
+    assert lib.qf_row_merged_supported(1, 1, 32, 8, 2560) == 0    # nothing to merge
+    assert lib.qf_row_merged_supported(1, 33, 32, 8, 2560) == 0   # more segments than a merge takes
+    assert lib.qf_row_merged_supported(4, 9, 128, 8, 512) == 0    # 4 x 16384 staged values
+    merged = lib.qf_linear_residual_merged
+    assert merged(bogus, bogus, 9, 1, 32, 8, bogus, 2560 + 256, bogus, bogus, bogus, None) == -2
+    assert merged(bogus, None, 9, 1, 32, 8, bogus, 2560, bogus, bogus, bogus, None) == -1
+    assert merged(bogus + 4, bogus, 9, 1, 32, 8, bogus, 2560, bogus, bogus, bogus, None) == -3
 
 
 def test_empty_inputs_are_no_ops():

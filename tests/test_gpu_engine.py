@@ -83,17 +83,23 @@ def check_teacher_forced(engine, prompts, tokens, logits):
 ROWS = dict(TINY, hidden_size=512, intermediate_size=1024)
 
 
-@pytest.mark.parametrize("batch", [1, 2, 3, 4])
-def test_folded_norms_match_native_and_the_split_path(batch):
-    """At 1-4 sequences the down projection adds the residual and the next
-    qkv projection normalises its input (no add + norm launch): teacher-forced
-    against native like the split-K path, and close to that path itself."""
+@pytest.mark.parametrize("batch,length", [(1, 21), (2, 21), (3, 21), (4, 21), (1, 300)])
+def test_folded_norms_match_native_and_the_split_path(batch, length, monkeypatch):
+    """With the fold on (batch 1 in the engine; here raised to 4 to cover
+    every row count) o_proj and down add the residual and gate/up and the
+    next qkv projection normalise their input (no add + norm launches):
+    teacher-forced against native like the split-K path, and close to that
+    path itself."""
+    import starter_amd.engine as engine_module
+    monkeypatch.setattr(engine_module, "FOLD_BATCH", 4)  # the engine folds batch 1 only by default
     cfg = Qwen3Config(**ROWS)
-    g = torch.Generator().manual_seed(7 + batch)
-    prompts = torch.randint(0, ROWS["vocab_size"], (batch, 21), generator=g).tolist()
+    g = torch.Generator().manual_seed(7 + batch + length)
+    prompts = torch.randint(0, ROWS["vocab_size"], (batch, length), generator=g).tolist()
     folded = Engine(config=cfg, seed=5, keep_logits=True)
     tokens, logits = run(folded, prompts, 5)
-    assert folded.state.fold_norms
+    assert folded.state.fold_norms and folded.state.fold_attention
+    if length == 300:
+        assert folded.state.attention.splits > 1
     check_teacher_forced(folded, prompts, tokens, logits)
     split = Engine(config=cfg, seed=5, keep_logits=True, fold_norms=False)
     split_tokens, split_logits = run(split, prompts, 5)
@@ -104,6 +110,24 @@ def test_folded_norms_match_native_and_the_split_path(batch):
     agree = torch.cat([torch.ones_like(same[:, :1]), same[:, :-1]], 1).bool()
     assert bool(agree[:, 1:].any())
     torch.testing.assert_close(logits[agree], split_logits[agree], rtol=0.02, atol=0.05)
+
+
+def test_folded_o_proj_merge_variants_agree(monkeypatch):
+    """The attention's segments merged inside o_proj (every workgroup) or by
+    the attention's own merge launch: the same bits either way."""
+    import starter_amd.engine as engine_module
+    cfg = Qwen3Config(**ROWS)
+    prompts = [list(range(3, 303))]
+    merge_in_o_proj = True
+    monkeypatch.setattr(engine_module, "MERGE_IN_O_PROJ", merge_in_o_proj)
+    eng = Engine(config=cfg, seed=5, keep_logits=True)
+    tokens, logits = run(eng, prompts, 4)
+    assert eng.state.fold_attention and eng.state.attention.splits > 1
+    monkeypatch.setattr(engine_module, "MERGE_IN_O_PROJ", not merge_in_o_proj)
+    other = Engine(config=cfg, seed=5, keep_logits=True)
+    other_tokens, other_logits = run(other, prompts, 4)
+    assert torch.equal(tokens, other_tokens)
+    assert torch.equal(logits, other_logits)
 
 
 def test_graph_replay_equals_eager(engine):

@@ -31,12 +31,14 @@ pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
 
 from starter_amd.kernels import row_gemv as rg  # noqa: E402
+from starter_amd.kernels.rotary import default_inv_freq, rope_tables  # noqa: E402
+from starter_amd.kernels.small_query_attention import SmallQueryAttention  # noqa: E402
 
 DEV = "cuda"
 QWEN = {"down": (2560, 9728), "qkv": (6144, 2560), "o": (2560, 4096)}
 CASES = [(rows, n, k) for rows in (1, 2, 3, 4) for n, k in
          [(2560, 9728), (6144, 2560), (2560, 4096), (512, 64), (8192, 256), (2048, 520)]
-         if (rows if rows <= 2 else 4) * (n // 256) <= 32]
+         if (rows if rows <= 2 else 4) * (n // 256) <= 128]
 
 
 def ints(shape, lo, hi, g):
@@ -86,8 +88,6 @@ def test_rows_integer_exact(rows, n, k):
 @pytest.mark.parametrize("name", ["down", "qkv", "o"])
 def test_rows_random_qwen_shapes(rows, name):
     n, k = QWEN[name]
-    if not (rows if rows <= 2 else 4) * (n // 256) <= 32:
-        pytest.skip("more outputs per workgroup than the kernel serves")
     g = gen(950 + rows)
     x, w = normal((rows, k), g=g), normal((n, k), std=0.02, g=g)
     xd, wd = x.to(DEV), w.to(DEV)
@@ -175,6 +175,94 @@ def test_normed_random_qkv_shape(rows):
     check_random(out, normed, w, f"normed rows={rows}")
 
 
+def sums_of_squares(total_bits, groups=256):
+    """f64 [rows, groups] whose row sums are the exact sums of squares."""
+    v = O.bf16_value(total_bits).astype(np.float64)
+    sq = np.zeros((v.shape[0], groups))
+    sq[:, 0] = (v * v).sum(-1)
+    return torch.from_numpy(sq)
+
+
+SILU_CASES = [(1, 9728, 2560), (1, 512, 256), (2, 1024, 512), (4, 512, 64), (3, 2048, 128)]
+
+
+@pytest.mark.parametrize("rows,n,k", SILU_CASES)
+def test_silu_normed_one_hot_exact(rows, n, k):
+    """One-hot gate and up rows pick elements of the normalised row: the
+    output must be the oracle's SiLU * up of exactly those elements."""
+    g = gen(1400 + rows + n)
+    total = normal((rows, k), std=2.0, g=g)
+    gain = normal((k,), mean=1.0, std=0.1, g=g)
+    w, perm = one_hot(2 * n, k, g)
+    out = rg.linear_silu_mul_normed(total.to(DEV), sums_of_squares(bits(total)).to(DEV),
+                                    gain.to(DEV), 1e-6, w.to(DEV))
+    torch.cuda.synchronize()
+    assert out.shape == (rows, n)
+    normed = O.rms_norm(bits(total), bits(gain), 1e-6)
+    want = O.silu_mul(np.concatenate([normed[:, perm[:n]], normed[:, perm[n:]]], axis=1))
+    assert_bits_exact(out, want, f"rows={rows} n={n} k={k}")
+
+
+@pytest.mark.parametrize("rows,n,k", SILU_CASES[:3])
+def test_silu_normed_random(rows, n, k):
+    g = gen(1450 + rows + n)
+    total = normal((rows, k), std=2.0, g=g)
+    gain = normal((k,), mean=1.0, std=0.1, g=g)
+    w = normal((2 * n, k), std=0.05, g=g)
+    out = rg.linear_silu_mul_normed(total.to(DEV), sums_of_squares(bits(total)).to(DEV),
+                                    gain.to(DEV), 1e-6, w.to(DEV))
+    normed = O.rms_norm(bits(total), bits(gain), 1e-6)
+    want = O.linear_silu_mul(normed, bits(w))
+    have_v, want_v = O.bf16_value(bits(out)), O.bf16_value(want)
+    np.testing.assert_allclose(have_v, want_v, rtol=2e-2, atol=2e-2)
+    assert float((bits(out) == want).mean()) >= 0.99
+
+
+SCALE = 128 ** -0.5
+MERGED_CASES = (  # b, hq, hk, cap, n, used rule
+    (1, 32, 8, 545, 2560, "full"),     # Qwen3-4B batch 1: 9 segments
+    (1, 32, 8, 1100, 2560, "full"),    # 18 segments: two batches in the merge
+    (2, 32, 8, 700, 2560, "mixed"),
+    (4, 8, 2, 300, 512, "mixed"),      # some heads attend nothing (zero rows)
+    (3, 16, 1, 193, 1024, "full"),     # 16 query rows per kv head
+)
+
+
+@pytest.mark.parametrize("b,hq,hk,cap,n,rule", MERGED_CASES)
+def test_residual_merged_equals_merge_then_residual(b, hq, hk, cap, n, rule):
+    """o_proj over the unmerged attention segments with the residual add
+    equals the attention's merged output through linear_residual, bit for bit."""
+    g = gen(1500 + cap + b)
+    qkv = (torch.randn((4, b, (hq + 2 * hk) * 128), generator=g) * 0.7).to(DEV)
+    qw, kw = normal((128,), 1.0, 0.1, g).to(DEV), normal((128,), 1.0, 0.1, g).to(DEV)
+    k, v = normal((b, hk, cap, 128), g=g).to(DEV), normal((b, hk, cap, 128), g=g).to(DEV)
+    w = normal((n, hq * 128), 0.0, 0.02, g).to(DEV)
+    residual = normal((b, n), std=2.0, g=g).to(DEV)
+    if rule == "full":
+        used = torch.full((b * hk,), cap, dtype=torch.int32)
+    else:
+        used = torch.arange(b * hk, dtype=torch.int32) * 97 % (cap + 1)
+        used[-1] = 0
+        used[0] = cap
+    used = used.to(DEV)
+    cos, sin = rope_tables(default_inv_freq(5_000_000.0, 128), cap, device=DEV)
+    plan = SmallQueryAttention(b, hq, hk, cap, DEV)
+    assert plan.splits > 1 and rg.supports_merged_shape(b, plan.splits, hq, hk, n)
+    position = torch.tensor([cap - 1], dtype=torch.int64, device=DEV)
+    k1, v1, k2, v2 = k.clone(), v.clone(), k.clone(), v.clone()
+    with torch.inference_mode():
+        attended = plan.run_qkv(qkv, qw, kw, 1e-6, 2e-6, cos, sin, position, k1, v1, used, SCALE)
+        want_total, want_sq = rg.linear_residual(attended.view(b, -1), w, residual)
+        plan.partials.fill_(float("nan"))  # only what the second call writes may be read
+        plan.stats.fill_(float("nan"))
+        plan.run_qkv_unmerged(qkv, qw, kw, 1e-6, 2e-6, cos, sin, position, k2, v2, used, SCALE)
+        total, sq = rg.linear_residual_merged(plan.partials, plan.stats, b, w, residual)
+    torch.cuda.synchronize()
+    assert_bits_exact(total, want_total, f"total (S={plan.splits})")
+    assert torch.equal(sq, want_sq)
+    assert_bits_exact(k2, k1, "key cache")
+
+
 def test_graph_replay_follows_fresh_inputs():
     g = gen(1300)
     (n, k), (n2, k2) = QWEN["down"], QWEN["qkv"]
@@ -211,7 +299,8 @@ def test_shape_rule():
     w = torch.zeros(2560, 9728, dtype=torch.bfloat16, device=DEV)
     assert rg.supports(torch.zeros(1, 9728, dtype=torch.bfloat16, device=DEV), w)
     assert not rg.supports(torch.zeros(5, 9728, dtype=torch.bfloat16, device=DEV), w)
-    assert not rg.supports(torch.zeros(3, 9728, dtype=torch.bfloat16, device=DEV), w)  # 4 x 10 > 32
+    assert rg.supports(torch.zeros(3, 9728, dtype=torch.bfloat16, device=DEV), w)  # 4 x 10 outputs
+    assert not rg.supports(torch.zeros(1, 9728, dtype=torch.bfloat16, device=DEV), w[:2304])  # 9 columns
     assert not rg.supports(torch.zeros(1, 9728, dtype=torch.float32, device=DEV), w)
     with pytest.raises(ValueError):
         rg.linear_rows(torch.zeros(1, 9720, dtype=torch.bfloat16, device=DEV), w[:, :9720])
