@@ -20,8 +20,9 @@ back-to-back launches of one kernel (rotating its buffer sets), divided by
 so the figure matches the kernel trace's average duration.  Decode
 configs 1-3 are timed the same way (microseconds per call), and so are the
 split-K decode projections of one Qwen3-4B layer at batch 1-64, beside the
-F.linear (hipBLASLt) path they replace, and decode attention at the engine
-contract's public workloads beside torch's scaled_dot_product_attention.  The CPU baseline
+F.linear (hipBLASLt) path they replace, decode attention at the engine
+contract's public workloads beside torch's scaled_dot_product_attention, and
+the causal prefill attention beside torch's flash kernel.  The CPU baseline
 (``cpu_baseline``) is the whole step through the reference's PyTorch formulas
 on the host CPU (up to 16 threads, CPU model stated); ``cpu_reference`` also
 times every BASELINE config that way, and ``cpu_baseline_oracle`` is the C
@@ -375,6 +376,50 @@ def decode_attention_bench(device, replays: int = 20, calls: int = GRAPH_CALLS) 
     return out
 
 
+#: Causal prefill attention at the Qwen3-4B heads (batch, prompt tokens).
+PREFILL_ATTENTION_CASES = ((4, 2048), (1, 4096), (16, 512))
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 matrix peak, AMD specification
+
+
+def prefill_attention_bench(device, replays: int = 20, calls: int = 8) -> dict:
+    """``prefill_attention`` (qf_prefill_attention) on the prompt's own cache
+    slots, beside torch's flash kernel on the same tensors (the reference's
+    prefill attention, engine/prefill.py:13-23).  Matrix-core bound: the
+    figure is causal flops (4 * B * Hq * T(T+1)/2 * 128) per second against
+    the dense bf16 peak."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from starter_amd.kernels.prefill import prefill_attention
+    g = torch.Generator(device=device).manual_seed(3)
+    out = {}
+    for batch, length in PREFILL_ATTENTION_CASES:
+        q = normal((batch, length, NQ, D), g=g)
+        keys = normal((batch, NK, length + 32, D), g=g)
+        values = normal((batch, NK, length + 32, D), g=g)
+        scale = D ** -0.5
+        flops = 4.0 * batch * NQ * (length * (length + 1) / 2) * D
+        t_ours = graph_time(lambda: prefill_attention(q, keys, values, length, scale), calls, replays)
+
+        def flash():
+            with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+                return torch.nn.functional.scaled_dot_product_attention(
+                    q.transpose(1, 2), keys[:, :, :length], values[:, :, :length], is_causal=True,
+                    scale=scale, enable_gqa=True)
+        try:
+            t_flash = graph_time(flash, calls, replays)
+        except RuntimeError:
+            t_flash = None
+        tflops = flops / (t_ours * 1e6)
+        key = f"b{batch}_t{length}"
+        out[key] = {"us_per_call": t_ours, "flops": flops, "tflops": tflops,
+                    "frac": tflops / PEAK_BF16_TFLOPS, "torch_flash_us": t_flash}
+        print(f"bench: prefill attention {key:10s} {t_ours:8.1f} us ({tflops:6.1f} TFLOP/s, "
+              f"{100 * tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak)  torch flash "
+              f"{t_flash if t_flash is None else round(t_flash, 1)} us", file=sys.stderr, flush=True)
+        del q, keys, values
+        torch.cuda.empty_cache()
+    return out
+
+
 #: The engine contract's public workloads (batch, prompt tokens, output tokens),
 #: plus batch 64: the largest batch the split-K decode projections serve.
 ENGINE_WORKLOADS = ((1, 512, 32), (4, 2048, 32), (16, 512, 128), (64, 512, 32))
@@ -719,6 +764,8 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true", help="skip the decode configs")
     ap.add_argument("--no-proj", action="store_true",
                     help="skip the decode projections and decode attention")
+    ap.add_argument("--no-prefill-attention", action="store_true",
+                    help="skip the causal prefill attention beside torch's flash kernel")
     ap.add_argument("--no-engine", action="store_true",
                     help="skip the end-to-end Qwen3-4B decode through starter_amd.engine")
     ap.add_argument("--engine-workload", metavar="B,T,N",
@@ -777,6 +824,7 @@ def main() -> int:
                   flush=True)
         projections = {} if args.no_proj else decode_projections(device)
         attention = {} if args.no_proj else decode_attention_bench(device)
+        prefill_attn = {} if args.no_prefill_attention else prefill_attention_bench(device)
     workloads = ENGINE_WORKLOADS
     if args.engine_workload:
         workloads = (tuple(int(v) for v in args.engine_workload.split(",")),)
@@ -812,6 +860,7 @@ def main() -> int:
         "decode": decode,
         "projections": projections,
         "attention": attention,
+        "prefill_attention": prefill_attn,
         "engine": engine,
         "copy_gbps": copy_gbps,
     }
