@@ -11,13 +11,16 @@
 // the flash kernel feeds them to its bf16 P V product) while l sums them in
 // f32; only O / l is rounded to bf16.
 //
-// Work split: a workgroup (4 waves) takes one (sequence, KV head) and 32
-// consecutive query positions for all G query heads of that KV head, i.e.
-// 2G tiles of 16 query rows (one head, 16 positions); wave w takes tiles w,
-// w + 4, ...  Workgroups run longest first (the last query blocks attend
-// the most keys).  Keys stream in blocks of 64, staged once per workgroup in
-// LDS (cooperative 16-byte loads, the next block's loads in flight during
-// this block's arithmetic) and shared by every tile.
+// Work split: a workgroup (W = 4 or 8 waves) takes one (sequence, KV head)
+// and QB consecutive query positions for all G query heads of that KV head,
+// i.e. G QB / 16 tiles of 16 query rows (one head, 16 positions); wave w
+// takes tiles w, w + W, ...  Workgroups run longest first (the last query
+// blocks attend the most keys).  Keys stream in blocks of 64, staged once per
+// workgroup in LDS (cooperative 16-byte loads into one of two buffers, the
+// next block's loads in flight during this block's arithmetic) and shared by
+// every tile, so the K/V bytes a CU pulls from L2 per flop shrink with the
+// workgroup's query rows (the per-CU L2 request rate, not the matrix cores,
+// bounded the 4-wave form).
 //
 // Both products are on the matrix cores (v_mfma_f32_16x16x32_bf16):
 // * Scores, transposed: S^T = K Q^T for a 16-key tile is a chain of four
@@ -58,7 +61,6 @@ constexpr int kKB = 64;                 // keys per staged block
 constexpr int kKRow = 272;              // LDS bytes per staged K row
 constexpr int kVRow = 288;              // LDS bytes per staged V row
 constexpr int kORow = 272;              // LDS bytes per row of the output staging tile
-constexpr int kLoadsPerThread = kKB * kD * 2 / 16 / kBlock;  // 16-byte loads per operand
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kLog2e = 1.4426950408889634f;
 // A row's exponent offset (its reference maximum, log2 units) is raised only
@@ -81,12 +83,21 @@ struct PrefillArgs {
 
 // Work split per group size G (query heads per KV head): QB query positions
 // per workgroup (a divisor of the key block, so a workgroup's queries share
-// one diagonal block) and TPW 16-row tiles per wave, G * QB / 16 = 4 TPW.
-template <int G> struct Split;
-template <> struct Split<1> { static constexpr int QB = 64, TPW = 1; };
-template <> struct Split<2> { static constexpr int QB = 64, TPW = 2; };
-template <> struct Split<4> { static constexpr int QB = 32, TPW = 2; };
-template <> struct Split<8> { static constexpr int QB = 16, TPW = 2; };
+// one diagonal block), W waves per workgroup and TPW 16-row tiles per wave,
+// G * QB / 16 = W * TPW.  Each staged key block serves all of a workgroup's
+// G * QB query rows, so its K/V traffic from L2 per flop falls as that grows:
+// at G = 4, 8 waves of 64 positions (256 rows) need half the block loads of
+// two 4-wave workgroups of 32 (the same two waves per SIMD).
+// WIDE (8 waves) is taken when the grid still has two workgroups per CU;
+// smaller prompts keep the 4-wave form's twice as many workgroups.
+template <int G, bool WIDE> struct Split;
+template <bool WIDE> struct Split<1, WIDE> { static constexpr int QB = 64, TPW = 1, W = 4; };
+template <bool WIDE> struct Split<2, WIDE> { static constexpr int QB = 64, TPW = 2, W = 4; };
+template <> struct Split<4, false> { static constexpr int QB = 32, TPW = 2, W = 4; };
+template <> struct Split<4, true> { static constexpr int QB = 64, TPW = 2, W = 8; };
+template <> struct Split<8, false> { static constexpr int QB = 16, TPW = 2, W = 4; };
+template <> struct Split<8, true> { static constexpr int QB = 32, TPW = 2, W = 8; };
+constexpr int64_t kWideWorkgroups = 2 * kCUs;
 
 __device__ __forceinline__ f32x4 mfma32(const uint4& a, const uint4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
@@ -98,12 +109,17 @@ __device__ __forceinline__ v4i16 read_tr(const uint8_t* base, int off) {
       (lds_v4i16*)((__attribute__((address_space(3))) uint8_t*)base + off));
 }
 
-template <int G>
-__global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
-  constexpr int QB = Split<G>::QB;
-  constexpr int TPW = Split<G>::TPW;
+template <int G, bool WIDE>
+__global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kernel(PrefillArgs a) {
+  constexpr int QB = Split<G, WIDE>::QB;
+  constexpr int TPW = Split<G, WIDE>::TPW;
+  constexpr int W = Split<G, WIDE>::W;
+  constexpr int kThreads = W * kWave;
   constexpr int kSubs = QB / 16;  // position tiles per head
-  static_assert(G * kSubs == 4 * TPW, "every wave holds TPW tiles");
+  constexpr int kLoadsPerThread = kKB * kD * 2 / 16 / kThreads;  // 16-byte loads per operand
+  static_assert(G * kSubs == W * TPW, "every wave holds TPW tiles");
+  static_assert(W % kSubs == 0, "a wave's tiles share their positions");
+  static_assert(W * 16 * kORow <= 2 * kKB * kKRow, "output staging fits the K buffers");
   // Two K/V block buffers: block j + 1 is staged into one while block j is
   // read from the other, so one barrier per block separates the two.
   __shared__ __attribute__((aligned(16))) uint8_t klds[2][kKB * kKRow];
@@ -125,16 +141,16 @@ __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
   const uint16_t* kbase = a.k + (int64_t)pair * a.capacity * kD;
   const uint16_t* vbase = a.v + (int64_t)pair * a.capacity * kD;
 
-  // This wave's tiles: tile tau = wave + 4u -> head kvh G + tau / kSubs,
+  // This wave's tiles: tile tau = wave + W u -> head kvh G + tau / kSubs,
   // positions p0 + 16 (tau % kSubs) .. +16 (the same positions for every
-  // tile of a wave, since kSubs divides 4).
+  // tile of a wave, since kSubs divides W).
   const int64_t pt = p0 + 16 * (wave % kSubs);
   int head[TPW];
   uint4 qf[TPW][4];
   const int64_t qpos = pt + r < a.length ? pt + r : last;
 #pragma unroll
   for (int u = 0; u < TPW; ++u) {
-    head[u] = kvh * G + (wave + 4 * u) / kSubs;
+    head[u] = kvh * G + (wave + W * u) / kSubs;
     const uint16_t* qr = a.q + (((int64_t)b * a.length + qpos) * a.q_heads + head[u]) * kD;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -154,13 +170,13 @@ __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
   }
 
   // Cooperative block loads: thread tid moves 16-byte chunk tid % 16 of keys
-  // tid / 16 + 16 i (i < 4) of the block, for K and for V.
+  // tid / 16 + (kThreads / 16) i of the block, for K and for V.
   uint4 kreg[kLoadsPerThread], vreg[kLoadsPerThread];
   const int chunk = tid % 16;
   auto fetch = [&](int j) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
-      int64_t key = (int64_t)j * kKB + tid / 16 + 16 * i;
+      int64_t key = (int64_t)j * kKB + tid / 16 + (kThreads / 16) * i;
       key = key < a.length ? key : last;
       kreg[i] = load16<true>(kbase + key * kD + 8 * chunk);
       vreg[i] = load16<true>(vbase + key * kD + 8 * chunk);
@@ -169,7 +185,7 @@ __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
   auto stage = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
-      const int key = tid / 16 + 16 * i;
+      const int key = tid / 16 + (kThreads / 16) * i;
       *reinterpret_cast<uint4*>(klds[buf] + key * kKRow + 16 * chunk) = kreg[i];
       *reinterpret_cast<uint4*>(vlds[buf] + key * kVRow + 16 * chunk) = vreg[i];
     }
@@ -279,7 +295,7 @@ __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
   // O / l in bf16, through LDS (this wave's 16 x 128 tile, one tile at a
   // time) so that every lane stores 16 contiguous bytes of one output row.
   __syncthreads();  // every wave is done with the K/V blocks
-  uint8_t* ot = klds[0] + wave * 16 * kORow;
+  uint8_t* ot = reinterpret_cast<uint8_t*>(klds) + wave * 16 * kORow;  // both K buffers
 #pragma unroll
   for (int u = 0; u < TPW; ++u) {
     float lt = lq[u] + __shfl_xor(lq[u], 16);
@@ -309,14 +325,22 @@ __global__ __launch_bounds__(kBlock) void prefill_attn_kernel(PrefillArgs a) {
   }
 }
 
-template <int G>
-int launch_prefill(PrefillArgs a, hipStream_t s) {
-  constexpr int QB = Split<G>::QB;
+template <int G, bool WIDE>
+int launch_prefill_as(PrefillArgs a, hipStream_t s) {
+  constexpr int QB = Split<G, WIDE>::QB;
   a.qblocks = (int32_t)((a.length + QB - 1) / QB);
   const int64_t blocks = (int64_t)a.qblocks * a.pairs;
   if (blocks > (int64_t)INT32_MAX) return QF_E_SHAPE;
-  hipLaunchKernelGGL((prefill_attn_kernel<G>), dim3((unsigned)blocks), dim3(kBlock), 0, s, a);
+  hipLaunchKernelGGL((prefill_attn_kernel<G, WIDE>), dim3((unsigned)blocks),
+                     dim3(Split<G, WIDE>::W * kWave), 0, s, a);
   return launch_status();
+}
+
+template <int G>
+int launch_prefill(PrefillArgs a, hipStream_t s) {
+  const int64_t wide_blocks = (a.length + Split<G, true>::QB - 1) / Split<G, true>::QB * a.pairs;
+  return wide_blocks >= kWideWorkgroups ? launch_prefill_as<G, true>(a, s)
+                                        : launch_prefill_as<G, false>(a, s);
 }
 
 }  // namespace

@@ -96,6 +96,23 @@ def test_monotone_scores(climb):
     check(out, q, k, v, t, f"climb={climb}")
 
 
+@pytest.mark.parametrize("b,t,hq,hk,seq,kvh", [
+    (4, 2048, 16, 4, 3, 1),   # G = 4: 512 workgroups of 64 positions (8 waves)
+    (4, 1024, 32, 4, 1, 3),   # G = 8: 512 workgroups of 32 positions (8 waves)
+])
+def test_wide_workgroups_match_oracle_slices(b, t, hq, hk, seq, kvh):
+    """Grids of >= 512 workgroups take the 8-wave form; one (sequence, KV
+    head) slice of its output against the float64 oracle of that slice."""
+    q, k, v = operands(b, t, hq, hk, t + 8, 880 + t + hq)
+    out = prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV), t, SCALE)
+    torch.cuda.synchronize()
+    g = hq // hk
+    heads = slice(kvh * g, (kvh + 1) * g)
+    check(out[seq:seq + 1, :, heads].cpu(), q[seq:seq + 1, :, heads].contiguous(),
+          k[seq:seq + 1, kvh:kvh + 1].contiguous(), v[seq:seq + 1, kvh:kvh + 1].contiguous(), t,
+          f"b{b} t{t} hq{hq} hk{hk} slice ({seq}, {kvh})")
+
+
 def test_zero_queries_give_the_running_mean():
     t, hk, hq = 100, 2, 8
     q = torch.zeros(1, t, hq, 128, dtype=torch.bfloat16, device=DEV)
