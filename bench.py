@@ -54,7 +54,7 @@ from starter_amd.kernels.prefill import prefill_qkv  # noqa: E402
 from starter_amd.kernels.qk_norm_rope import qk_norm_rope  # noqa: E402
 from starter_amd.kernels.rmsnorm import rms_norm  # noqa: E402
 from starter_amd.kernels.rotary import default_inv_freq, rope_tables  # noqa: E402
-from starter_amd.kernels import skinny_gemm  # noqa: E402
+from starter_amd.kernels import row_gemv, skinny_gemm  # noqa: E402
 from starter_amd.kernels.small_query_attention import SmallQueryAttention  # noqa: E402
 
 METRIC = ("achieved HBM GB/s (% of MI355X peak) + µs/call per fused kernel, decode & prefill")
@@ -296,7 +296,9 @@ PROJECTION_ROWS = (1, 4, 16, 64)
 def decode_projections(device, replays: int = 20, calls: int = GRAPH_CALLS) -> dict:
     """Split-K projections (linear_partials / linear_silu_mul) at decode batch
     1-64 on the Qwen3-4B layer shapes, next to the unfused path the engine
-    takes without them (F.linear on hipBLASLt, plus silu_mul for gate/up).
+    takes without them (F.linear on hipBLASLt, plus silu_mul for gate/up),
+    and at batch 1 the one-workgroup-per-CU forms the engine runs there
+    (row_gemv, with the add or norm of the neighbouring add + norm folded in).
     Weights rotate over enough copies to exceed twice the Infinity Cache, as
     in decode, where 36 layers of weights (7.3 GB) stream from HBM each step."""
     g = torch.Generator(device=device).manual_seed(1)
@@ -325,6 +327,28 @@ def decode_projections(device, replays: int = 20, calls: int = GRAPH_CALLS) -> d
                               "hipblaslt_us": t_base, "speedup_vs_hipblaslt": t_base / t_ours}
             print(f"bench: proj {name:8s} m={m:2d} {t_ours:7.2f} us ({100 * entry[f'm{m}']['frac']:.1f}% "
                   f"of peak)  F.linear path {t_base:7.2f} us", file=sys.stderr, flush=True)
+        # The engine's batch-1 form: whole-K workgroups, one per CU, with the
+        # residual add (o_proj, down) or the RMSNorm (qkv; gate/up with SiLU)
+        # folded in (no add + norm launch between projections).
+        x = normal((1, k), g=g)
+        sq = torch.ones((1, row_gemv.GROUPS), dtype=torch.float64, device=device)
+        gain = normal((k,), 1.0, 0.1, g)
+        if name == "gate_up":
+            fold = lambda i: row_gemv.linear_silu_mul_normed(x, sq, gain, 1e-6, weights[i % len(weights)])
+            kind, out_bytes = "norm prologue + SiLU*up", bf16_bytes(n)
+        elif name == "qkv":
+            fold = lambda i: row_gemv.linear_normed(x, sq, gain, 1e-6, weights[i % len(weights)])
+            kind, out_bytes = "norm prologue", bf16_bytes(n)
+        else:
+            residual = normal((1, n), g=g)
+            fold = lambda i: row_gemv.linear_residual(x, weights[i % len(weights)], residual)
+            kind, out_bytes = "residual epilogue", bf16_bytes(2 * n) + 8 * row_gemv.GROUPS
+        t_fold = graph_time_rotating(fold, calls, replays)
+        moved = w_bytes + bf16_bytes(k) + out_bytes
+        entry["m1_folded"] = {"us_per_call": t_fold, "bytes": moved, "kind": kind,
+                              "gbps": moved / (t_fold * 1e3), "frac": moved / (t_fold * 1e3) / PEAK_GBPS}
+        print(f"bench: proj {name:8s} m= 1 {t_fold:7.2f} us ({100 * entry['m1_folded']['frac']:.1f}% "
+              f"of peak)  one workgroup per CU, {kind}", file=sys.stderr, flush=True)
         out[name] = entry
         del weights
         torch.cuda.empty_cache()
