@@ -21,10 +21,10 @@ reference runs:
   key segments itself), the fused gate/up projection with its SiLU epilogue, and
   the LM head fused with the greedy token choice; at batch 1 the
   projections run one workgroup per compute unit over the whole K range,
-  so both residual adds move into the epilogues of o_proj (which also merges
-  the attention's key segments) and down, and both RMSNorms into the
-  prologues of gate/up and the next qkv projection (two launches fewer per
-  layer, bit-identical normalised rows); the whole step is
+  so both residual adds move into the epilogues of o_proj and down, and
+  both RMSNorms into the prologues of gate/up and the next qkv projection
+  (two launches fewer per layer, bit-identical normalised rows; at batch 2
+  the down / next-qkv pair only, one launch fewer); the whole step is
   captured once per (batch, capacity) in a HIP graph and replayed with the
   position and cache lengths advanced on the device.
 
@@ -129,10 +129,14 @@ def check_rotary(model) -> None:
 #: Largest batch whose decode step merges attention segments inside o_proj.
 MERGED_O_BATCH = 1
 #: Largest batch whose decode step folds the add + norm launches into the
-#: one-workgroup-per-CU projections (measured: batch 1 1,989 against 2,121
-#: us/step with the down/qkv fold alone and ~2,190 with neither; at batch 4
-#: the 4-row projections lose to the split-K ones, 2,434 against 2,396).
-FOLD_BATCH = 1
+#: one-workgroup-per-CU projections where their shapes allow (measured:
+#: batch 1 1,989 against 2,121 us/step with the down/qkv fold alone and
+#: ~2,190 with neither; batch 2, where only the down/qkv fold fits (the SiLU
+#: epilogue serves 128 outputs per workgroup), 2,134-2,145 against
+#: 2,194-2,196 at 512 prompt tokens and 2,213-2,217 against 2,274-2,278 at
+#: 2,048; batch 3, padded to 4 rows, 2,249-2,262 against 2,221-2,225, and
+#: batch 4 2,438 against 2,397: there the split-K projections win).
+FOLD_BATCH = 2
 #: Whether the folded path merges the attention's segments inside o_proj
 #: (every workgroup merges every head: 2,154 us/step at batch 1) instead of
 #: taking the attention's own merge launch (1,989 us/step).
@@ -198,9 +202,9 @@ class Engine:
                  keep_logits: bool = False, fold_norms: bool = True):
         """``keep_logits``: also keep each step's bf16 logits in ``last_logits``
         (a device copy per step; for tests and inspection).  ``fold_norms``:
-        up to FOLD_BATCH sequences fold both add + norm launches of a layer
-        into the projections around them (off: the split-K path at every
-        batch)."""
+        up to FOLD_BATCH sequences fold the add + norm launches of a layer
+        into the projections around them where the shapes allow (off: the
+        split-K path at every batch)."""
         from transformers import Qwen3ForCausalLM
         self.device = torch.device(device)
         if self.device.type != "cuda" or not torch.cuda.is_available():
