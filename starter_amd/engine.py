@@ -126,7 +126,10 @@ def check_rotary(model) -> None:
                          f"with attention_scaling {scaling}")
 
 
-#: Largest batch whose decode step merges attention segments inside o_proj.
+#: Largest batch whose decode step merges attention segments inside o_proj
+#: (split-K path; every column tile re-merges its heads' segments, so larger
+#: batches lose: 2,806 against 2,389 us/step at 4 x 2048, 3,364 against 2,480
+#: at 8 x 1024, 4,468 against 2,669 at 16 x 512, same tokens).
 MERGED_O_BATCH = 1
 #: Largest batch whose decode step folds the add + norm launches into the
 #: one-workgroup-per-CU projections where their shapes allow (measured:
