@@ -312,6 +312,36 @@ int qf_linear_silu_mul_normed(const void* total, const double* sq, const void* g
                               void* stream);
 
 /*
+ * The same normalisation on the matrix-core projections instead of the row
+ * kernels: the consumers of a qf_linear_residual producer (its total and sq)
+ * at 1..4 rows, as many workgroups as qf_linear_partials /
+ * qf_linear_silu_mul launch.  Each workgroup first normalises the rows'
+ * slice of its own K range into LDS (x = bf16(bf16(total * inv) * gain) with
+ * inv = 1 / sqrt(f32(sum_g sq[r][g]) / k + eps), the rounding steps of
+ * qf_add_rms_norm) while its first weight chunks are in flight, then runs
+ * the tiles of the plain entry point, so the result is bit-identical to
+ * qf_linear_partials / qf_linear_silu_mul called on the row qf_add_rms_norm
+ * writes.  They replace, like qf_linear_normed
+ * and qf_linear_silu_mul_normed, add_rms_norm (engine/kernels/
+ * decode_fused.py:140-160) followed by linear_partials / linear_silu_mul
+ * (engine/kernels/skinny_gemm.py:100-121) at engine/decode_step.py:43-44
+ * and :53.
+ *
+ * total bf16 [rows, k], gain bf16 [k] and the weight 16-byte aligned, sq f64
+ * [rows, QF_ROW_GROUPS] 8-byte aligned; 1 <= rows <= 4; k % 64 == 0 and
+ * n % 32 == 0 as qf_linear_partials (splits as there); the slice,
+ * rows * k / splits values (qf_linear_silu_mul_normed_tiled: rows * k), at
+ * most 10,240.  Otherwise QF_E_SHAPE / QF_E_ARG / QF_E_ALIGN as the plain
+ * entry points.
+ */
+int qf_linear_partials_normed(const void* total, const double* sq, const void* gain, float eps,
+                              int64_t rows, int64_t k, const void* weight, int64_t n,
+                              int32_t splits, void* partials, void* stream);
+int qf_linear_silu_mul_normed_tiled(const void* total, const double* sq, const void* gain,
+                                    float eps, int64_t rows, int64_t k, const void* gate_up,
+                                    int64_t n, void* out, void* stream);
+
+/*
  * Key-segment plan of qf_decode_attention for virtual_heads = batch * Hkv
  * heads of a cache with `capacity` slots on a GPU with compute_units CUs:
  * at most one workgroup per CU, segments of whole 64-key tiles, at most 32.

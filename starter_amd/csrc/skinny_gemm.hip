@@ -71,6 +71,8 @@ constexpr int kEpiArgmax = 2;    // bf16 logits (optional) + argmax candidates p
 constexpr int kXDirect = 0;  // global loads straight into MFMA layout (up to 4 rows)
 constexpr int kXStaged = 1;  // loaded like W, transposed through the wave's LDS tile
 constexpr int kXMerged = 2;  // merged from attention segments into LDS by a prologue
+constexpr int kXNormed = 3;  // RMSNorm of the residual stream, into LDS by a prologue
+constexpr int kNormRows = 4; // most rows kXNormed takes (f64 sums of squares per thread)
 
 // Is (v, i) ahead of (bv, bi) in argmax order: larger value, NaN above
 // everything, the lower index on equal values (torch.argmax's first maximum)?
@@ -97,6 +99,13 @@ struct SkinnyArgs {
   int32_t seg_splits;
   int32_t seg_groups;
   int32_t seg_kv_heads;
+  // kXNormed only: x (the residual stream `total`, bf16 [m, k]) enters as
+  //   inv = 1 / sqrt(f32(sum_g sq[m][g]) / k + eps),  bf16(bf16(x * inv) * gain)
+  // with sq f64 [m, QF_ROW_GROUPS] (per-workgroup sums of squares from
+  // qf_linear_residual) and gain bf16 [k].
+  const double* sq;
+  const uint16_t* gain;
+  float eps;
 };
 
 __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, const f32x4& c) {
@@ -254,23 +263,32 @@ __device__ __forceinline__ void finish(const SkinnyArgs& a, f32x4 (&acc)[NT][MT]
 // taken from the two halves of the weight); the four waves
 // form WN = 4/WK groups of distinct n-tiles, each group WK waves that split
 // the chunks; D chunks in flight per wave; NTL = nontemporal weight loads;
-// XS = source of x (kXDirect, kXStaged, kXMerged).  Waves of different
-// groups read the same x chunk at about the same time, so x is fetched from
-// L2 once per workgroup rather than once per wave.
+// XS = source of x (kXDirect, kXStaged, kXMerged, kXNormed).  Waves of
+// different groups read the same x chunk at about the same time, so x is
+// fetched from L2 once per workgroup rather than once per wave.
 //
 // kXMerged (MT = 1): the workgroup's x slice, M rows x (chunks * 64)
 // columns = whole heads of the attention output, is merged from the
 // attention segments by the workgroup itself into dynamic LDS (row stride
 // chunks * 128 + 16 bytes), one wave per (row, head), after the first D
 // weight chunks are issued, so the merge's loads overlap the weight loads.
-template <int MT, int NT, int WK, int D, int EPI, bool NTL, int XS>
+// kXNormed (M <= kNormRows): the same slice, normalised from the residual
+// stream with qf_add_rms_norm's rounding steps (inverse RMS from the
+// producer's per-workgroup sums of squares) into the same LDS layout, PPT
+// 16-byte pieces per thread.  MFMA operands and their order are those of
+// kXDirect: a normalised x equal to qf_add_rms_norm's output gives the bits
+// of qf_linear_partials / qf_linear_silu_mul on it.
+template <int MT, int NT, int WK, int D, int EPI, bool NTL, int XS, int PPT = 0>
 __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
   constexpr bool PAIRS = EPI == kEpiSiluMul;
   constexpr bool HALF = PAIRS && NT == 1;
   constexpr bool XT = XS == kXStaged;
   constexpr bool XM = XS == kXMerged;
+  constexpr bool XN = XS == kXNormed;
+  constexpr bool XL = XM || XN;  // x read from the prologue's LDS slice
   static_assert(kWaves % WK == 0, "wave split");
-  static_assert(!XM || MT == 1, "merged x holds at most 16 rows");
+  static_assert(!XL || MT == 1, "an LDS x slice holds at most 16 rows");
+  static_assert(!XN || (kBlock == QF_ROW_GROUPS && PPT >= 1), "normed x: one sum per thread and row");
   constexpr int WN = kWaves / WK;
   constexpr int kCols = PAIRS ? NT / 2 : NT;  // output n-tiles per wave
   constexpr int kColW = HALF ? kTile / 2 : kTile * kCols;  // output columns per wave
@@ -280,6 +298,7 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
   __shared__ __attribute__((aligned(16)))
       uint8_t lds[kStageBytes > kHandoffBytes ? kStageBytes : kHandoffBytes];
   extern __shared__ __attribute__((aligned(16))) uint8_t xm_lds[];
+  __shared__ double xn_wsum[XN ? kWaves : 1][kNormRows];
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -313,7 +332,7 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
       if constexpr (XT) {  // coalesced like W, transposed through LDS
         const int row = kTile * mt + kRowsPerLoad * i + lane / 8;
         xp[mt][i] = a.x + (int64_t)(row < a.m ? row : 0) * a.k + kbase + 8 * (lane % 8);
-      } else if constexpr (!XM) {  // straight into MFMA layout
+      } else if constexpr (!XL) {  // straight into MFMA layout
         const int row = kTile * mt + r;
         xp[mt][i] = a.x + (int64_t)(row < a.m ? row : 0) * a.k + kbase + 8 * g + kStep * i;
       }
@@ -340,11 +359,76 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int i = 0; i < 2; ++i) wv[d][t][i] = load16<NTL>(wp[t] + off + i * wstep);
-    if constexpr (!XM) {
+    if constexpr (!XL) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 2; ++i) xv[d][mt][i] = load16<false>(xp[mt][i] + off);
+    }
+  };
+  // The normed-x prologue: 16-byte piece p of the slice is row p / per_row,
+  // columns kbase + 8 * (p % per_row) .. +8.  Thread t loads sq[q][t] of
+  // every row q and its PPT pieces t, t + 256, ... (x and gain) before the
+  // first weight loads - a fixed count with no branch, so the waits below
+  // cover only these loads and the weight chunks stay in flight; pieces past
+  // the slice re-read piece 0 and are not stored.  After the weight loads the
+  // f64 sums are reduced (in wave, then wave order through LDS: exact) and
+  // the pieces normalised into the LDS slice.
+  const int xn_per_row = a.chunks * (kChunk / 8);
+  const int xn_pieces = XN ? a.m * xn_per_row : 0;
+  double sqv[XN ? kNormRows : 1];
+  uint4 xnv[XN ? PPT : 1], gnv[XN ? PPT : 1];
+  auto norm_first = [&]() {
+    if constexpr (XN) {
+#pragma unroll
+      for (int q = 0; q < kNormRows; ++q)
+        sqv[q] = a.sq[(int64_t)(q < a.m ? q : 0) * QF_ROW_GROUPS + threadIdx.x];
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const int p = (int)threadIdx.x + kBlock * i;
+        const int pc = p < xn_pieces ? p : 0;
+        const int row = pc / xn_per_row, col = pc - row * xn_per_row;
+        xnv[i] = load16<false>(a.x + (int64_t)row * a.k + kbase + 8 * col);
+        gnv[i] = load16<false>(a.gain + kbase + 8 * col);
+      }
+    }
+  };
+  auto norm_x = [&]() {
+    if constexpr (XN) {
+#pragma unroll
+      for (int q = 0; q < kNormRows; ++q) sqv[q] = group_sum_f64<kWave>(sqv[q]);
+      if (lane == 0) {
+#pragma unroll
+        for (int q = 0; q < kNormRows; ++q) xn_wsum[wave][q] = sqv[q];
+      }
+      __syncthreads();
+      float inv[kNormRows];
+#pragma unroll
+      for (int q = 0; q < kNormRows; ++q) {
+        double sum = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) sum += xn_wsum[w][q];
+        inv[q] = inv_rms(sum, (float)a.k, a.eps);
+      }
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const int p = (int)threadIdx.x + kBlock * i;
+        const int row = p / xn_per_row, col = p - row * xn_per_row;
+        float iv = inv[0];
+#pragma unroll
+        for (int q = 1; q < kNormRows; ++q) iv = row == q ? inv[q] : iv;
+        // The rounding steps of qf_add_rms_norm: bf16(bf16(t * inv) * gain).
+        float f[8], gf[8];
+        unpack8(xnv[i], f);
+        unpack8(gnv[i], gf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] *= iv;
+        round8(f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] *= gf[e];
+        if (p < xn_pieces) *reinterpret_cast<uint4*>(xm_lds + row * xm_row + 16 * col) = pack8(f);
+      }
+      __syncthreads();
     }
   };
   // The merged-x prologue: wave w merges (row, head) pairs w, w + 4, ... of
@@ -408,7 +492,7 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
       for (int mt = 0; mt < MT; ++mt) {
         if constexpr (XT)
           fx[mt][s] = *reinterpret_cast<const uint4*>(stage + (NT + mt) * kTileLds + rd_off[s]);
-        else if constexpr (XM)
+        else if constexpr (XL)
           fx[mt][s] = *reinterpret_cast<const uint4*>(xm_lds + xm_off + (wk + WK * j) * kChunk * 2 + s * kStep * 2);
         else
           fx[mt][s] = xv[d][mt][s];
@@ -427,10 +511,12 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
   // unconditionally, so the compiler's wait counts stay exact (each consume
   // waits only for its own chunk); only the last 2*D chunks take branches.
   merge_first();
+  norm_first();
   if (n_own >= D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(d, d);
     merge_x();
+    norm_x();
     int j = 0;
     for (; j + 2 * D <= n_own; j += D) {
 #pragma unroll
@@ -453,6 +539,7 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
     for (int d = 0; d < D; ++d)
       if (d < n_own) issue(d, d);
     merge_x();
+    norm_x();
 #pragma unroll
     for (int d = 0; d < D; ++d)
       if (d < n_own) consume(d, d);
@@ -664,15 +751,32 @@ int plan_splits(int64_t rows, int64_t k, int64_t n) {
   return (int)s;
 }
 
-template <int MT, int NT, int WK, int D, int EPI, bool NTL, int XS>
+template <int MT, int NT, int WK, int D, int EPI, bool NTL, int XS, int PPT = 0>
 int launch(const SkinnyArgs& a, int splits, hipStream_t s, size_t dyn_lds = 0) {
   constexpr bool PAIRS = EPI == kEpiSiluMul;
   constexpr int kColsPerBlock =
       (PAIRS && NT == 1 ? kTile / 2 : kTile * (PAIRS ? NT / 2 : NT)) * (kWaves / WK);
   const int64_t grid_x = (a.n + kColsPerBlock - 1) / kColsPerBlock;
-  hipLaunchKernelGGL((skinny_kernel<MT, NT, WK, D, EPI, NTL, XS>),
+  hipLaunchKernelGGL((skinny_kernel<MT, NT, WK, D, EPI, NTL, XS, PPT>),
                      dim3((unsigned)grid_x, (unsigned)splits), dim3(kBlock), dyn_lds, s, a);
   return launch_status();
+}
+
+// The normed-x kernels, instantiated for 1..kMaxPiecesPerThread slice pieces
+// per thread (the prologue's loads are a fixed count).
+constexpr int kMaxPiecesPerThread = 5;  // 4 rows x 2560 columns of slice
+template <int D, int EPI>
+int launch_normed(const SkinnyArgs& a, int splits, hipStream_t s) {
+  const int64_t pieces = (int64_t)a.m * a.chunks * (kChunk / 8);
+  const size_t lds = (size_t)a.m * (size_t)(a.chunks * kChunk * 2 + 16);
+  switch ((pieces + kBlock - 1) / kBlock) {
+    case 1: return launch<1, 1, 4, D, EPI, true, kXNormed, 1>(a, splits, s, lds);
+    case 2: return launch<1, 1, 4, D, EPI, true, kXNormed, 2>(a, splits, s, lds);
+    case 3: return launch<1, 1, 4, D, EPI, true, kXNormed, 3>(a, splits, s, lds);
+    case 4: return launch<1, 1, 4, D, EPI, true, kXNormed, 4>(a, splits, s, lds);
+    case 5: return launch<1, 1, 4, D, EPI, true, kXNormed, 5>(a, splits, s, lds);
+    default: return QF_E_SHAPE;
+  }
 }
 
 template <int MT, int NT, int WK, int D, int EPI>
@@ -980,6 +1084,66 @@ extern "C" int qf_linear_partials_merged(const float* seg_partials, const float*
   // qf_linear_partials for up to 16 rows: one 16-row x tile, four waves
   // splitting each workgroup's chunks, two chunks in flight.
   return launch<1, 1, 4, 2, kEpiPartials, true, kXMerged>(a, splits, as_stream(stream), lds);
+}
+
+namespace qf {
+namespace {
+// Checks and arguments shared by the normed-input entry points.
+int normed_args(SkinnyArgs& a, const void* total, const double* sq, const void* gain, float eps,
+                int64_t rows, int64_t k, const void* weight, int64_t n, int64_t chunks) {
+  const int st = shape_status(rows, k, n);
+  if (st != QF_OK) return st;
+  if (rows > kNormRows || rows * chunks * (kChunk / 8) > (int64_t)kMaxPiecesPerThread * kBlock)
+    return QF_E_SHAPE;
+  if (!total || !sq || !gain || !weight) return QF_E_ARG;
+  if (!(eps == eps) || eps < 0.0f || eps == __builtin_inff()) return QF_E_ARG;
+  if (!aligned16(total) || !aligned16(gain) || !aligned16(weight) ||
+      (reinterpret_cast<uintptr_t>(sq) & 7u) != 0)
+    return QF_E_ALIGN;
+  a = SkinnyArgs{};
+  a.x = static_cast<const uint16_t*>(total);
+  a.w = static_cast<const uint16_t*>(weight);
+  a.k = k;
+  a.m = (int32_t)rows;
+  a.n = (int32_t)n;
+  a.chunks = (int32_t)chunks;
+  a.sq = sq;
+  a.gain = static_cast<const uint16_t*>(gain);
+  a.eps = eps;
+  return QF_OK;
+}
+}  // namespace
+}  // namespace qf
+
+extern "C" int qf_linear_partials_normed(const void* total, const double* sq, const void* gain,
+                                         float eps, int64_t rows, int64_t k, const void* weight,
+                                         int64_t n, int32_t splits, void* partials, void* stream) {
+  if (splits < 1 || k <= 0 || k % kChunk != 0 || (k / kChunk) % splits != 0) return QF_E_ARG;
+  SkinnyArgs a;
+  const int st = normed_args(a, total, sq, gain, eps, rows, k, weight, n, k / kChunk / splits);
+  if (st != QF_OK) return st;
+  if (!partials) return QF_E_ARG;
+  if (!aligned16(partials)) return QF_E_ALIGN;
+  a.partials = static_cast<float*>(partials);
+  // qf_linear_partials' plan for up to 4 rows (the same tiles, waves and
+  // chunks in flight, so the same f32 addition order).
+  return launch_normed<2, kEpiPartials>(a, splits, as_stream(stream));
+}
+
+extern "C" int qf_linear_silu_mul_normed_tiled(const void* total, const double* sq,
+                                               const void* gain, float eps, int64_t rows,
+                                               int64_t k, const void* gate_up, int64_t n,
+                                               void* out, void* stream) {
+  if (k <= 0 || k % kChunk != 0) return QF_E_SHAPE;
+  SkinnyArgs a;
+  const int st = normed_args(a, total, sq, gain, eps, rows, k, gate_up, n, k / kChunk);
+  if (st != QF_OK) return st;
+  if (!out) return QF_E_ARG;
+  if ((reinterpret_cast<uintptr_t>(out) & 7u) != 0) return QF_E_ALIGN;
+  a.out = static_cast<uint16_t*>(out);
+  // qf_linear_silu_mul's plan for up to 4 rows: 8 gate over 8 up rows per
+  // workgroup, four waves splitting K, four chunks in flight.
+  return launch_normed<4, kEpiSiluMul>(a, 1, as_stream(stream));
 }
 
 extern "C" int qf_linear_silu_mul(const void* x, int64_t rows, int64_t k, const void* gate_up,

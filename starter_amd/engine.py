@@ -24,7 +24,8 @@ reference runs:
   so both residual adds move into the epilogues of o_proj and down, and
   both RMSNorms into the prologues of gate/up and the next qkv projection
   (two launches fewer per layer, bit-identical normalised rows; at batch 2
-  the down / next-qkv pair only, one launch fewer); the whole step is
+  gate/up normalises its input inside the split-K matrix-core tiles
+  instead, whose row kernel cannot serve two rows); the whole step is
   captured once per (batch, capacity) in a HIP graph and replayed with the
   position and cache lengths advanced on the device.
 
@@ -58,7 +59,8 @@ from .kernels.rmsnorm import rms_norm
 from .kernels.rotary import rope_tables
 from .kernels import row_gemv
 from .kernels.skinny_gemm import (linear_partials, linear_partials_merged, linear_silu_mul,
-                                  supports, supports_merged)
+                                  linear_silu_mul_normed, supports, supports_merged,
+                                  supports_normed_shape)
 from .kernels.small_query_attention import SmallQueryAttention
 
 HEAD = 128
@@ -132,18 +134,26 @@ def check_rotary(model) -> None:
 #: at 8 x 1024, 4,468 against 2,669 at 16 x 512, same tokens).
 MERGED_O_BATCH = 1
 #: Largest batch whose decode step folds the add + norm launches into the
-#: one-workgroup-per-CU projections where their shapes allow (measured:
+#: projections around them where their shapes allow (measured on Qwen3-4B:
 #: batch 1 1,989 against 2,121 us/step with the down/qkv fold alone and
-#: ~2,190 with neither; batch 2, where only the down/qkv fold fits (the SiLU
-#: epilogue serves 128 outputs per workgroup), 2,134-2,145 against
-#: 2,194-2,196 at 512 prompt tokens and 2,213-2,217 against 2,274-2,278 at
-#: 2,048; batch 3, padded to 4 rows, 2,249-2,262 against 2,221-2,225, and
-#: batch 4 2,438 against 2,397: there the split-K projections win).
+#: ~2,190 with neither; batch 2 with both folds - gate/up on the normalising
+#: matrix-core tiles - 2,092-2,096 against 2,135-2,139 with the down/qkv fold
+#: alone and 2,194-2,196 with neither at 512 prompt tokens, 2,168-2,170
+#: against 2,214-2,221 at 2,048; batch 3 2,199-2,229 against 2,214-2,216
+#: and batch 4 2,262-2,275 against 2,262-2,264 with both folds: no gain).
 FOLD_BATCH = 2
 #: Whether the folded path merges the attention's segments inside o_proj
 #: (every workgroup merges every head: 2,154 us/step at batch 1) instead of
 #: taking the attention's own merge launch (1,989 us/step).
 MERGE_IN_O_PROJ = False
+#: Whether the folded path's gate/up projection may run as the matrix-core
+#: tiles with the RMSNorm in their prologue (``skinny_gemm.linear_silu_mul_normed``)
+#: where the one-workgroup-per-CU kernel's SiLU epilogue cannot serve the
+#: batch (2 rows x 76 columns per workgroup).  At batch 1 the row kernel
+#: stays (18.7 us against 18.9 for the tiles on Qwen3-4B, whose plain form
+#: takes 16.9: every workgroup's prologue reads the same sums of squares,
+#: row and gain at once), and so does qkv (7.7 against 10.3 us).
+NORMED_TILES = True
 
 
 class _State:
@@ -180,8 +190,11 @@ class _State:
         o_ok = (row_gemv.supports_merged_shape(batch, splits, engine.q_heads, engine.kv_heads,
                                                hidden) if MERGE_IN_O_PROJ and splits > 1 else
                 row_gemv.supports_shape(batch, first.o.shape[1], hidden))
+        row_silu = row_gemv.supports_silu_shape(batch, hidden, inner)
+        self.tiled_gate_up = (NORMED_TILES and not row_silu
+                              and supports_normed_shape(batch, hidden, inner, pairs=True))
         self.fold_attention = (engine.fold_norms and batch <= FOLD_BATCH and o_ok
-                               and row_gemv.supports_silu_shape(batch, hidden, inner))
+                               and (row_silu or self.tiled_gate_up))
         self.prompt = torch.zeros((batch, length), dtype=torch.int64, device=dev)
         self.tokens = torch.zeros(batch, dtype=torch.int64, device=dev)
         self.position = torch.zeros(1, dtype=torch.int64, device=dev)
@@ -369,8 +382,9 @@ class Engine:
                 else:
                     attended = st.attention.run_qkv(*args).view(batch, -1)
                     x, sq = row_gemv.linear_residual(attended, layer.o, x)
-                hidden = row_gemv.linear_silu_mul_normed(x, sq, layer.ln_post, layer.eps_post,
-                                                         layer.gate_up)
+                normed_mlp = (linear_silu_mul_normed if st.tiled_gate_up
+                              else row_gemv.linear_silu_mul_normed)
+                hidden = normed_mlp(x, sq, layer.ln_post, layer.eps_post, layer.gate_up)
             else:
                 if st.merged_o:
                     st.attention.run_qkv_unmerged(*args)

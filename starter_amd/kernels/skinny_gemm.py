@@ -15,6 +15,11 @@ third argument because the split plan here depends on it.
 * ``linear_silu_mul(x, gate_up_weight)``: ``bf16(silu(bf16(gate)) * bf16(up))``
   for a packed ``[2N, K]`` weight, with both projections and the SiLU epilogue
   in one launch.
+* ``linear_partials_normed`` / ``linear_silu_mul_normed``: the same two at 1-4
+  rows for x = RMSNorm of the residual stream, normalised by each workgroup
+  from the per-workgroup sums of squares ``row_gemv.linear_residual`` writes
+  (no add + norm launch before them); bit-identical to the plain calls on
+  ``add_rms_norm``'s normalised row.
 
 Both launch one HIP kernel on torch's current stream (no host sync, no device
 value read), so the engine's graph capture of the decode step takes them
@@ -22,6 +27,8 @@ unchanged.  There is no fallback: without the HIP library every call raises.
 """
 
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -140,6 +147,70 @@ def linear_partials_merged(partials, stats, batch, weight):
     _lib.call("qf_linear_partials_merged", partials.data_ptr(), stats.data_ptr(), segments, batch,
               q_heads, kv_heads, weight.data_ptr(), n, splits, out.data_ptr(),
               _lib.stream(weight.device))
+    return out
+
+
+#: Most rows the normalising projections take; sums of squares per row.
+NORMED_MAX_ROWS = 4
+SQ_GROUPS = 256
+
+
+def _normed_dims(total, sq, gain, eps, weight, pairs):
+    """(rows, k, n) of a normalising call, raising ValueError like the
+    plain calls for shapes, dtypes and layouts they do not take."""
+    if not supports(total, weight, pairs) or total.shape[0] > NORMED_MAX_ROWS:
+        raise ValueError("expected contiguous BF16 CUDA total[1..4, K] and W[N, K] with "
+                         "tile-aligned N, K")
+    rows, k = total.shape
+    if (sq.shape != (rows, SQ_GROUPS) or sq.dtype != torch.float64 or sq.device != total.device
+            or not sq.is_contiguous()):
+        raise ValueError("sq must be a contiguous float64 [rows, 256] tensor on total's device")
+    if (gain.shape != (k,) or gain.dtype != torch.bfloat16 or gain.device != total.device
+            or not gain.is_contiguous() or not _aligned(gain)):
+        raise ValueError("gain must be a contiguous BF16 [K] tensor on total's device")
+    if not (math.isfinite(eps) and eps >= 0):
+        raise ValueError("eps must be finite and non-negative")
+    n = weight.shape[0] // 2 if pairs else weight.shape[0]
+    return rows, k, n
+
+
+def supports_normed_shape(rows, k, n, pairs=False):
+    """Shape rule of the normalising calls for total [rows, k] against W [n, k]
+    (``pairs``: a packed gate/up weight of 2n rows): the plain rule at 1-4
+    rows, and each workgroup's normalised slice (rows x K / splits, whole K
+    for gate/up) at most 10,240 values (5 16-byte pieces per thread)."""
+    if not (1 <= rows <= NORMED_MAX_ROWS and k > 0 and n > 0 and k % BK == 0 and n % BN == 0):
+        return False
+    per_split = k if pairs else k // split_count(n, k, rows)
+    return rows * per_split <= 10240
+
+
+def linear_partials_normed(total, sq, gain, eps, weight):
+    """``linear_partials(RMSNorm(total), weight)`` with the norm applied inside
+    the projection: x = bf16(bf16(total * inv) * gain), inv from ``sq`` (the
+    f64 [rows, 256] sums of squares ``row_gemv.linear_residual`` wrote for
+    ``total``).  Same split plan and bits as the plain call on that x."""
+    rows, k, n = _normed_dims(total, sq, gain, eps, weight, False)
+    splits = split_count(n, k, rows)
+    if not supports_normed_shape(rows, k, n):
+        raise ValueError("the normalised slice of this shape exceeds 10,240 values per workgroup")
+    partials = torch.empty((splits, rows, n), dtype=torch.float32, device=total.device)
+    _lib.call("qf_linear_partials_normed", total.data_ptr(), sq.data_ptr(), gain.data_ptr(),
+              float(eps), rows, k, weight.data_ptr(), n, splits, partials.data_ptr(),
+              _lib.stream(total.device))
+    return partials
+
+
+def linear_silu_mul_normed(total, sq, gain, eps, gate_up_weight):
+    """``linear_silu_mul(RMSNorm(total), gate_up_weight)`` with the norm as in
+    ``linear_partials_normed``; returns BF16 [rows, N]."""
+    rows, k, n = _normed_dims(total, sq, gain, eps, gate_up_weight, True)
+    if not supports_normed_shape(rows, k, n, pairs=True):
+        raise ValueError("the normalised row of this shape exceeds 10,240 values per workgroup")
+    out = torch.empty((rows, n), dtype=torch.bfloat16, device=total.device)
+    _lib.call("qf_linear_silu_mul_normed_tiled", total.data_ptr(), sq.data_ptr(), gain.data_ptr(),
+              float(eps), rows, k, gate_up_weight.data_ptr(), n, out.data_ptr(),
+              _lib.stream(total.device))
     return out
 
 

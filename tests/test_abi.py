@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 29
+    assert len(names) == 31
 
 
 def test_library_exports_every_symbol():
@@ -180,6 +180,26 @@ def test_host_side_argument_errors_launch_nothing():
     assert silu(bogus, None, bogus, 1e-6, 1, 2560, bogus, 9728, bogus, None) == -1
     assert silu(bogus, bogus, bogus, float("inf"), 1, 2560, bogus, 9728, bogus, None) == -1
     assert silu(bogus, bogus + 4, bogus, 1e-6, 1, 2560, bogus, 9728, bogus, None) == -3
+    # the same norm on the matrix-core tiles: 1..4 rows, the plain tile rules,
+    # at most 10,240 slice values per workgroup
+    pn = lib.qf_linear_partials_normed
+    assert pn(bogus, bogus, bogus, 1e-6, 5, 2560, bogus, 6144, 8, bogus, None) == -2
+    assert pn(bogus, bogus, bogus, 1e-6, 1, 2560, bogus, 6144 + 16, 8, bogus, None) == -2
+    assert pn(bogus, bogus, bogus, 1e-6, 1, 2560, bogus, 6144, 3, bogus, None) == -1
+    assert pn(bogus, None, bogus, 1e-6, 1, 2560, bogus, 6144, 8, bogus, None) == -1
+    assert pn(bogus, bogus, bogus, float("nan"), 1, 2560, bogus, 6144, 8, bogus, None) == -1
+    assert pn(bogus, bogus + 4, bogus, 1e-6, 1, 2560, bogus, 6144, 8, bogus, None) == -3
+    assert pn(bogus + 8, bogus, bogus, 1e-6, 1, 2560, bogus, 6144, 8, bogus, None) == -3
+    assert pn(bogus, bogus, bogus, 1e-6, 1, 2560, bogus, 6144, 8, None, None) == -1
+    assert pn(bogus, bogus, bogus, 1e-6, 4, 4096, bogus, 2560, 1, bogus, None) == -2  # 16,384 values
+    st = lib.qf_linear_silu_mul_normed_tiled
+    assert st(bogus, bogus, bogus, 1e-6, 5, 2560, bogus, 9728, bogus, None) == -2
+    assert st(bogus, bogus, bogus, 1e-6, 1, 2560 + 8, bogus, 9728, bogus, None) == -2
+    assert st(bogus, bogus, None, 1e-6, 1, 2560, bogus, 9728, bogus, None) == -1
+    assert st(bogus, bogus, bogus, -1.0, 1, 2560, bogus, 9728, bogus, None) == -1
+    assert st(bogus, bogus, bogus + 8, 1e-6, 1, 2560, bogus, 9728, bogus, None) == -3
+    assert st(bogus, bogus, bogus, 1e-6, 1, 2560, bogus, 9728, bogus + 4, None) == -3
+    assert st(bogus, bogus, bogus, 1e-6, 4, 4096, bogus, 2560, bogus, None) == -2
     # o_proj over the attention segments with the residual add
     assert lib.qf_row_merged_supported(1, 9, 32, 8, 2560) == 1
     assert lib.qf_row_merged_supported(1, 1, 32, 8, 2560) == 0    # nothing to merge

@@ -112,6 +112,23 @@ def test_folded_norms_match_native_and_the_split_path(batch, length, monkeypatch
     torch.testing.assert_close(logits[agree], split_logits[agree], rtol=0.02, atol=0.05)
 
 
+@pytest.mark.parametrize("batch,length", [(1, 21), (2, 300)])
+def test_folded_norms_with_tiled_gate_up(batch, length, monkeypatch):
+    """Where the one-workgroup-per-CU SiLU epilogue cannot serve the batch
+    (Qwen3-4B at batch 2; forced here) gate/up normalises its input inside
+    the matrix-core tiles: teacher-forced against native like the other
+    paths."""
+    import starter_amd.engine as engine_module
+    monkeypatch.setattr(engine_module.row_gemv, "supports_silu_shape", lambda *args: False)
+    cfg = Qwen3Config(**ROWS)
+    g = torch.Generator().manual_seed(17 + batch + length)
+    prompts = torch.randint(0, ROWS["vocab_size"], (batch, length), generator=g).tolist()
+    folded = Engine(config=cfg, seed=5, keep_logits=True)
+    tokens, logits = run(folded, prompts, 5)
+    assert folded.state.fold_attention and folded.state.tiled_gate_up
+    check_teacher_forced(folded, prompts, tokens, logits)
+
+
 def test_default_fold_rule():
     """The engine folds the add + norm launches up to batch 2 and keeps the
     split-K path from batch 3 (3 rows would run padded to 4)."""
