@@ -445,8 +445,10 @@ def prefill_attention_bench(device, replays: int = 20, calls: int = 8) -> dict:
 
 
 #: The engine contract's public workloads (batch, prompt tokens, output tokens),
-#: plus batch 64: the largest batch the split-K decode projections serve.
-ENGINE_WORKLOADS = ((1, 512, 32), (4, 2048, 32), (16, 512, 128), (64, 512, 32))
+#: plus batch 2 (the largest batch whose decode step folds the add + norm
+#: launches into its projections) and batch 64 (the largest batch the split-K
+#: decode projections serve).
+ENGINE_WORKLOADS = ((1, 512, 32), (2, 512, 32), (4, 2048, 32), (16, 512, 128), (64, 512, 32))
 
 
 def engine_decode(device, steps: int = 32, workloads=ENGINE_WORKLOADS) -> dict:
