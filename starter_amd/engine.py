@@ -17,8 +17,7 @@ reference runs:
 * decode (``engine/decode_step.py:33-64``): the split-K projections whose f32
   partials feed ``add_rms_norm`` and the split-KV decode attention (which
   also does ``qkv_norm_rope_cache``'s Q/K norm, RoPE and cache write in its
-  own launches; at small batches the o_proj projection merges the attention's
-  key segments itself), the fused gate/up projection with its SiLU epilogue, and
+  own launches), the fused gate/up projection with its SiLU epilogue, and
   the LM head fused with the greedy token choice; at batch 1 the
   projections run one workgroup per compute unit over the whole K range,
   so both residual adds move into the epilogues of o_proj and down, and
