@@ -500,15 +500,21 @@ def engine_decode(device, steps: int = 32, workloads=ENGINE_WORKLOADS) -> dict:
         kv = 36 * batch * NK * mid * D * 2 * 2 + 36 * batch * NK * D * 2 * 2
         step_bytes = weight_bytes + kv + bf16_bytes(batch * H)
         key = f"b{batch}_p{length}"
+        # the engine contract's figure for the whole workload (QWEN_ENGINE_CONTRACT.md:88-94):
+        # batch x output tokens / (time to the first tokens + the remaining
+        # steps), here from the warm first-token time and the measured step
+        total_s = t_prefill + (new - 1) * step_us * 1e-6
         out[key] = {"decode_steps": done, "us_per_step": step_us,
                     "tokens_per_s": batch / (step_us * 1e-6),
+                    "output_tokens": new, "workload_tokens_per_s": batch * new / total_s,
                     "prefill_ms": t_prefill * 1e3, "prefill_tokens_per_s": batch * length / t_prefill,
                     "first_call_s": t_first,
                     "step_bytes": step_bytes, "gbps": step_bytes / (step_us * 1e3),
                     "frac": step_bytes / (step_us * 1e3) / PEAK_GBPS}
         print(f"bench: engine {key:10s} decode {step_us:8.1f} us/step  {out[key]['tokens_per_s']:8.1f} tok/s "
               f"({100 * out[key]['frac']:.1f}% of HBM roofline)  prefill {t_prefill * 1e3:.2f} ms warm "
-              f"({t_first:.2f} s first call, with allocation and capture)",
+              f"({t_first:.2f} s first call, with allocation and capture)  "
+              f"{out[key]['workload_tokens_per_s']:.0f} tok/s for {batch} x {new} output tokens",
               file=sys.stderr, flush=True)
     del engine
     torch.cuda.empty_cache()
