@@ -44,7 +44,9 @@ engine needs a GPU and the HIP library.
 
 from __future__ import annotations
 
+from contextlib import contextmanager
 from dataclasses import dataclass
+from pathlib import Path
 
 import torch
 from torch import nn
@@ -145,6 +147,40 @@ FOLD_BATCH = 2
 #: (every workgroup merges every head: 2,154 us/step at batch 1) instead of
 #: taking the attention's own merge launch (1,989 us/step).
 MERGE_IN_O_PROJ = False
+#: hipBLASLt solutions for the prefill projections where one measured faster
+#: than the library's default choice on MI355X (torch TunableOp's results
+#: format, read with tuning switched off; torch checks the file's torch, HIP,
+#: hipBLASLt and GPU versions and ignores it when they differ).  One entry:
+#: the Qwen3-4B gate/up projection at 8,192 prompt rows, 586 against 667 us
+#: with the weights streamed from HBM; the other projections at 512, 2,048
+#: and 8,192 rows gained nothing.
+TUNED_GEMMS = Path(__file__).with_name("tuned_gemms_gfx950.csv")
+_tuned_gemms_loaded: bool | None = None
+
+
+@contextmanager
+def tuned_gemms(active: bool = True):
+    """Within the block, torch's projections take the recorded solutions of
+    ``TUNED_GEMMS`` (TunableOp on, tuning off; every other shape keeps the
+    default choice); TunableOp's previous switches are restored after.  A
+    HIP graph captured inside keeps the chosen kernels for its replays."""
+    global _tuned_gemms_loaded
+    tunable = torch.cuda.tunable
+    if active and _tuned_gemms_loaded is None:
+        _tuned_gemms_loaded = TUNED_GEMMS.exists() and bool(tunable.read_file(str(TUNED_GEMMS)))
+    if not (active and _tuned_gemms_loaded):
+        yield
+        return
+    previous = (tunable.is_enabled(), tunable.tuning_is_enabled())
+    tunable.tuning_enable(False)
+    tunable.enable(True)
+    try:
+        yield
+    finally:
+        tunable.enable(previous[0])
+        tunable.tuning_enable(previous[1])
+
+
 #: Whether the folded path's gate/up projection may run as the matrix-core
 #: tiles with the RMSNorm in their prologue (``skinny_gemm.linear_silu_mul_normed``)
 #: where the one-workgroup-per-CU kernel's SiLU epilogue cannot serve the
@@ -214,12 +250,14 @@ class Engine:
 
     def __init__(self, model_path: str | None = None, *, config=None, seed: int = 0,
                  device: str | torch.device = "cuda", use_graphs: bool = True,
-                 keep_logits: bool = False, fold_norms: bool = True):
+                 keep_logits: bool = False, fold_norms: bool = True, tuned_gemms: bool = True):
         """``keep_logits``: also keep each step's bf16 logits in ``last_logits``
         (a device copy per step; for tests and inspection).  ``fold_norms``:
         up to FOLD_BATCH sequences fold the add + norm launches of a layer
         into the projections around them where the shapes allow (off: the
-        split-K path at every batch)."""
+        split-K path at every batch).  ``tuned_gemms``: the prefill's
+        projections take the recorded hipBLASLt solutions of TUNED_GEMMS
+        where one exists for their shape."""
         from transformers import Qwen3ForCausalLM
         self.device = torch.device(device)
         if self.device.type != "cuda" or not torch.cuda.is_available():
@@ -253,6 +291,7 @@ class Engine:
         self.use_graphs = use_graphs
         self.keep_logits = keep_logits
         self.fold_norms = fold_norms
+        self.tuned_gemms = tuned_gemms
         self.state: _State | None = None
         self.last_logits = None
         # One side stream for every warm-up and capture: torch keeps a BLAS
@@ -336,18 +375,20 @@ class Engine:
         (warm-up runs first, then capture, then the replay that produces the
         result), as engine/prefill.py:79-99 does; eager when graphs are off."""
         if not st.graphable:
-            return self._prefill(st)
+            with tuned_gemms(self.tuned_gemms):
+                return self._prefill(st)
         if st.prefill_graph is None:
             current = torch.cuda.current_stream(self.device)
             stream = self._capture_stream
             stream.wait_stream(current)
-            with torch.cuda.stream(stream):
-                for _ in range(2):
-                    self._prefill(st)
-            current.wait_stream(stream)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
-                st.prefill_logits = self._prefill(st)
+            with tuned_gemms(self.tuned_gemms):
+                with torch.cuda.stream(stream):
+                    for _ in range(2):
+                        self._prefill(st)
+                current.wait_stream(stream)
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    st.prefill_logits = self._prefill(st)
             current.wait_stream(stream)
             st.prefill_graph = graph
         st.prefill_graph.replay()

@@ -51,3 +51,17 @@ def test_engine_needs_a_gpu():
         pytest.skip("this host has a GPU")
     with pytest.raises(RuntimeError):
         engine.Engine(config=Qwen3Config(**TINY))
+
+
+def test_tuned_gemms_file_is_a_tunableop_table():
+    """The recorded prefill solutions: TunableOp's CSV (validator lines, then
+    op, shape key, solution, time) with one entry per shape."""
+    from starter_amd.engine import TUNED_GEMMS
+    lines = TUNED_GEMMS.read_text().splitlines()
+    validators = [line.split(",") for line in lines if line.startswith("Validator,")]
+    assert {v[1] for v in validators} >= {"PT_VERSION", "GCN_ARCH_NAME", "HIPBLASLT_VERSION"}
+    assert any(v[1] == "GCN_ARCH_NAME" and v[2].startswith("gfx950") for v in validators)
+    entries = [line.split(",") for line in lines if line and not line.startswith("Validator,")]
+    assert entries and all(len(e) == 4 and e[0].startswith("GemmTunableOp_") for e in entries)
+    assert len({e[1] for e in entries}) == len(entries)
+    assert all(float(e[3]) > 0 for e in entries)

@@ -226,3 +226,25 @@ def test_one_state_at_a_time():
             assert engine.state.key == (batch, length, count)
     for first, second in seen.values():
         assert second <= first
+
+
+def test_tuned_gemms_serve_the_prefill_gate_up_shape():
+    """Inside ``tuned_gemms`` the recorded hipBLASLt solution serves the
+    Qwen3-4B prefill gate/up shape (8,192 rows) - within bf16 GEMM rounding of
+    the default choice - and TunableOp's switches are restored after."""
+    import torch.nn.functional as F
+    from starter_amd import engine as engine_module
+    tunable = torch.cuda.tunable
+    before = (tunable.is_enabled(), tunable.tuning_is_enabled())
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(8192, 2560, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(19456, 2560, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    want = F.linear(x, w)
+    with engine_module.tuned_gemms(True):
+        assert tunable.is_enabled() and not tunable.tuning_is_enabled()
+        got = F.linear(x, w)
+    assert (tunable.is_enabled(), tunable.tuning_is_enabled()) == before
+    assert any(r[1].startswith("tn_19456_8192_2560_") for r in tunable.get_results())
+    torch.testing.assert_close(got.float(), want.float(), rtol=2e-2, atol=2e-2)
+    with engine_module.tuned_gemms(False):
+        assert (tunable.is_enabled(), tunable.tuning_is_enabled()) == before
