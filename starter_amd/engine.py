@@ -167,7 +167,10 @@ def tuned_gemms(active: bool = True):
     global _tuned_gemms_loaded
     tunable = torch.cuda.tunable
     if active and _tuned_gemms_loaded is None:
-        _tuned_gemms_loaded = TUNED_GEMMS.exists() and bool(tunable.read_file(str(TUNED_GEMMS)))
+        try:
+            _tuned_gemms_loaded = TUNED_GEMMS.exists() and bool(tunable.read_file(str(TUNED_GEMMS)))
+        except RuntimeError:  # a torch build without TunableOp, or a table it cannot parse
+            _tuned_gemms_loaded = False
     if not (active and _tuned_gemms_loaded):
         yield
         return
