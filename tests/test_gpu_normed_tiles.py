@@ -113,3 +113,42 @@ def test_inputs_unchanged_and_shape_rule():
     with pytest.raises(ValueError):
         sk.linear_silu_mul_normed(total.repeat(5, 1), sq.repeat(5, 1), gain, 1e-6,
                                   normal((1024, k), g=gen(1802)).to(DEV))
+
+
+@torch.inference_mode()
+def test_graph_replay_follows_fresh_inputs():
+    """The residual producer and both normalising tiles captured in one HIP
+    graph (as in the batch-2 decode step): every replay with new inputs, with
+    eager work between the replays, equals the eager calls bit for bit."""
+    rows, k_in, width = 2, 512, 2560
+    g = gen(1900)
+    x = normal((rows, k_in), g=g).to(DEV)
+    w_res = normal((width, k_in), std=0.05, g=g).to(DEV)
+    residual = normal((rows, width), std=2.0, g=g).to(DEV)
+    gain = normal((width,), mean=1.0, std=0.1, g=g).to(DEV)
+    w_qkv = normal((1024, width), std=0.05, g=g).to(DEV)
+    gate_up = normal((2 * 1024, width), std=0.05, g=g).to(DEV)
+
+    def step():
+        total, sq = rg.linear_residual(x, w_res, residual)
+        return (sk.linear_partials_normed(total, sq, gain, 1e-6, w_qkv),
+                sk.linear_silu_mul_normed(total, sq, gain, 1e-6, gate_up))
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        outputs = step()
+    torch.cuda.synchronize()
+    for replay in range(4):
+        x.copy_(normal((rows, k_in), g=g).to(DEV))
+        residual.copy_(normal((rows, width), std=2.0, g=g).to(DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = step()
+        torch.cuda.synchronize()
+        assert torch.equal(outputs[0].view(torch.int32), want[0].view(torch.int32)), replay
+        assert torch.equal(outputs[1].view(torch.int16), want[1].view(torch.int16)), replay
