@@ -140,9 +140,12 @@ MERGED_O_BATCH = 1
 #: ~2,190 with neither; batch 2 with both folds - gate/up on the normalising
 #: matrix-core tiles - 2,092-2,096 against 2,135-2,139 with the down/qkv fold
 #: alone and 2,194-2,196 with neither at 512 prompt tokens, 2,168-2,170
-#: against 2,214-2,221 at 2,048; batch 3 2,199-2,229 against 2,214-2,216
-#: and batch 4 2,262-2,275 against 2,262-2,264 with both folds: no gain).
-FOLD_BATCH = 2
+#: against 2,214-2,221 at 2,048.  With the normalising prologues waiting for
+#: the sums of squares only: batch 3 2,136-2,187 against 2,213-2,216 at 512
+#: prompt tokens, 2,249-2,294 against 2,324-2,326 at 2,048; batch 4
+#: 2,251-2,263 against 2,258-2,262 at 512 and 2,392-2,394 against
+#: 2,392-2,394 at 2,048: no gain there).
+FOLD_BATCH = 3
 #: Whether the folded path merges the attention's segments inside o_proj
 #: (every workgroup merges every head: 2,154 us/step at batch 1) instead of
 #: taking the attention's own merge launch (1,989 us/step).

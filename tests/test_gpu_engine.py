@@ -85,13 +85,13 @@ ROWS = dict(TINY, hidden_size=512, intermediate_size=1024)
 
 @pytest.mark.parametrize("batch,length", [(1, 21), (2, 21), (3, 21), (4, 21), (1, 300)])
 def test_folded_norms_match_native_and_the_split_path(batch, length, monkeypatch):
-    """With the fold on (batch <= 2 in the engine; here raised to 4 to cover
+    """With the fold on (batch <= 3 in the engine; here raised to 4 to cover
     every row count) o_proj and down add the residual and gate/up and the
     next qkv projection normalise their input (no add + norm launches):
     teacher-forced against native like the split-K path, and close to that
     path itself."""
     import starter_amd.engine as engine_module
-    monkeypatch.setattr(engine_module, "FOLD_BATCH", 4)  # the engine folds batch <= 2 by default
+    monkeypatch.setattr(engine_module, "FOLD_BATCH", 4)  # the engine folds batch <= 3 by default
     cfg = Qwen3Config(**ROWS)
     g = torch.Generator().manual_seed(7 + batch + length)
     prompts = torch.randint(0, ROWS["vocab_size"], (batch, length), generator=g).tolist()
@@ -130,10 +130,10 @@ def test_folded_norms_with_tiled_gate_up(batch, length, monkeypatch):
 
 
 def test_default_fold_rule():
-    """The engine folds the add + norm launches up to batch 2 and keeps the
-    split-K path from batch 3 (3 rows would run padded to 4)."""
+    """The engine folds the add + norm launches up to batch 3 (3 rows run
+    padded to 4 on the row kernels) and keeps the split-K path from batch 4."""
     eng = Engine(config=Qwen3Config(**ROWS), seed=5)
-    for batch, folded in ((1, True), (2, True), (3, False), (4, False)):
+    for batch, folded in ((1, True), (2, True), (3, True), (4, False)):
         prompt = [[(3 * i + j) % ROWS["vocab_size"] for j in range(9)] for i in range(batch)]
         assert len(list(eng.generate(prompt, 2))) == 2
         assert eng.state.fold_norms == folded, batch
