@@ -126,6 +126,55 @@ __device__ __forceinline__ void merge_lanes(State<GT>& s, int mask) {
   }
 }
 
+// The bf16-row form of fused_prologue in two halves, so a caller can issue
+// other loads between the prologue's loads and their use.
+struct PrologueLoads {
+  uint4 wv, cv, sv, xv;
+};
+
+__device__ __forceinline__ PrologueLoads prologue_issue(const AttnArgs& a, int vh, int lg, int r,
+                                                        int rows, int64_t pos) {
+  const int G = a.groups;
+  const int64_t hkv = a.kv_heads;
+  const int64_t b = vh / hkv, h = vh - b * hkv;
+  const int64_t hq = hkv * G;
+  const int64_t width = (hq + 2 * hkv) * kD;
+  const int64_t slot = pos >= 0 && pos < a.capacity ? pos : 0;
+  const bool is_q = lg < rows, is_k = lg == 8;
+  const int64_t head = is_q ? h * G + a.g0 + lg : is_k ? hq + h : hq + hkv + h;
+  PrologueLoads L;
+  L.wv = load16<false>((is_q ? a.qw : a.kw) + 8 * r);
+  L.cv = load16<false>(a.cos + slot * kD + 8 * r);
+  L.sv = load16<false>(a.sin + slot * kD + 8 * r);
+  // every lane group loads a row of its virtual head (the value row when it
+  // holds none), so the load count is fixed
+  L.xv = load16<false>(static_cast<const uint16_t*>(a.qkv) + b * width + head * kD + 8 * r);
+  return L;
+}
+
+__device__ __forceinline__ bool prologue_finish(const AttnArgs& a, const PrologueLoads& L, int vh,
+                                                int lg, int r, int rows, int64_t start, int64_t pos,
+                                                uint4 (*qs)[16], uint4 (*kvs)[16]) {
+  const bool pos_ok = pos >= 0 && pos < a.capacity;
+  const bool is_q = lg < rows, is_k = lg == 8, is_v = lg == 9;
+  // Lane groups without a row of their own work on the value row they
+  // loaded (nothing of theirs is stored), so the load is used by every lane
+  // and the compiler cannot sink it under a branch.
+  const uint4 xv = L.xv;
+  float x[8];
+  unpack8(xv, x);
+  const uint4 o = norm_rope(x, L.wv, L.cv, L.sv, is_q ? a.q_eps : a.k_eps, r);  // every lane: DPP
+  const uint4 nan4 = make_uint4(0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u);
+  if (is_q) qs[lg][r] = select4(pos_ok, o, nan4);
+  if (is_k) kvs[0][r] = o;
+  if (is_v) kvs[1][r] = xv;
+  const bool owns_slot = pos_ok && pos >= start && pos < start + a.span;
+  if (owns_slot && a.g0 == 0 && (is_k || is_v))
+    store16<false>((is_k ? a.kc : a.vc) + ((int64_t)vh * a.capacity + pos) * kD + 8 * r,
+                   select4(is_k, o, xv));
+  return owns_slot;
+}
+
 // Fused Q/K/V prologue (qf_decode_attention_qkv), run by every lane of the
 // workgroup before the key loop: lane group lg (16 lanes = one DPP row, lane
 // r holding elements 8r..8r+8) folds or loads one packed row of virtual head
@@ -470,11 +519,16 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
   const int64_t start = (int64_t)seg * a.span;
   int64_t end = start + a.span;
   if (end > used) end = used;
-  const uint16_t* kbase = a.k + (int64_t)vh * a.capacity * kD;
-  const uint16_t* vbase = a.v + (int64_t)vh * a.capacity * kD;
+  // The fused bf16-row path issues its first key blocks whether or not the
+  // wave has keys (their loads are discarded then); a head with no valid key
+  // at all reads them from the query gain (128 values, in bounds for every
+  // lane's offsets), so no cache slot at or beyond used is ever read.
+  const bool dummy = FUSED && used == 0;
+  const uint16_t* kbase = dummy ? a.qw : a.k + (int64_t)vh * a.capacity * kD;
+  const uint16_t* vbase = dummy ? a.qw : a.v + (int64_t)vh * a.capacity * kD;
   const int64_t nb = end > start ? (end - start + 15) / 16 : 0;  // 16-key blocks of the segment
   const int n = nb > wave ? (int)((nb - wave + kW - 1) / kW) : 0;
-  const int64_t last_key = end - 1;  // a valid slot whenever n > 0
+  const int64_t last_key = end > 0 ? end - 1 : 0;  // below used whenever used > 0
 
   // Query rows as the scores' B operand: column = lane % 16 (< G), k = dims
   // 8*(lane/16) + 32 s.
@@ -501,13 +555,24 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
       vf[d][u] = load16<NTL>(vbase + vk * kD + 8 * r);
     }
   };
-  if (n > 0) {
-#pragma unroll
-    for (int d = 0; d + 1 < NS; ++d) issue(d, d);
-  }
   if constexpr (FUSED) {
     pos = pos_in;
-    const bool owns_slot = fused_prologue(a, vh, wave * 4 + q4, r, rows, start, pos, qs, kvs);
+    bool owns_slot;
+    if (a.qkv_splits == 0) {
+      // bf16 rows: the prologue's loads, then the first key blocks (issued
+      // unconditionally, so the prologue waits for its own loads only and
+      // its arithmetic overlaps the key loads).
+      const PrologueLoads pl = prologue_issue(a, vh, wave * 4 + q4, r, rows, pos);
+#pragma unroll
+      for (int d = 0; d + 1 < NS; ++d) issue(d, d);
+      owns_slot = prologue_finish(a, pl, vh, wave * 4 + q4, r, rows, start, pos, qs, kvs);
+    } else {
+      if (n > 0) {
+#pragma unroll
+        for (int d = 0; d + 1 < NS; ++d) issue(d, d);
+      }
+      owns_slot = fused_prologue(a, vh, wave * 4 + q4, r, rows, start, pos, qs, kvs);
+    }
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < 4; ++s) qa[s] = r < rows ? qs[r][q4 + 4 * s] : make_uint4(0, 0, 0, 0);
@@ -516,6 +581,11 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) knew[s] = kvs[0][q4 + 4 * s];
       vnew = kvs[1][r];
+    }
+  } else {
+    if (n > 0) {
+#pragma unroll
+      for (int d = 0; d + 1 < NS; ++d) issue(d, d);
     }
   }
 

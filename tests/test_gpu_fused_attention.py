@@ -71,6 +71,8 @@ CASES = (  # b, hq, hk, cap, qkv splits, position, used rule
     (1, 4, 4, 64, 1, 63, "pos+1"),          # one query row per kv head
     (2, 4, 2, 100, 2, 99, "mixed"),
     (16, 32, 8, 641, 4, 640, "pos+1"),      # Qwen3-4B batch 16
+    (1, 32, 8, 545, 0, 544, "pos+1"),       # Qwen3-4B batch 1 from bf16 rows (the folded step)
+    (3, 6, 2, 257, 0, 63, "empty"),         # bf16 rows; mixed lengths and a head with no key
 )
 
 
@@ -82,6 +84,8 @@ def test_fused_equals_the_call_pair_bit_for_bit(b, hq, hk, cap, splits, pos, rul
     else:
         used = torch.arange(b * hk, dtype=torch.int32) * 53 % (cap + 1)
         used[0] = pos + 1
+        if rule == "empty":
+            used[1] = 0  # a head with no key: zeros, and no NaN from the poisoned cache
     cos, sin = rope_tables(INV_FREQ, cap, device=DEV)
     plan = SmallQueryAttention(b, hq, hk, cap, DEV)
     kp, vp = poison(k, used).to(DEV), poison(v, used).to(DEV)
