@@ -152,6 +152,58 @@ __device__ __forceinline__ PrologueLoads prologue_issue(const AttnArgs& a, int v
   return L;
 }
 
+// The split-K form for up to kPrologueSplits partials: every lane loads a
+// partial of its row for each of the kPrologueSplits slots (slots past the
+// split count re-read the last split and are not added), so the count is
+// fixed; the sum runs in split order as sum_partials8's does.
+constexpr int kPrologueSplits = 8;
+struct PartialLoads {
+  uint4 wv, cv, sv;
+  float4 lo[kPrologueSplits], hi[kPrologueSplits];
+};
+
+__device__ __forceinline__ PartialLoads partials_issue(const AttnArgs& a, int vh, int lg, int r,
+                                                       int rows, int64_t pos) {
+  const int G = a.groups;
+  const int64_t hkv = a.kv_heads;
+  const int64_t b = vh / hkv, h = vh - b * hkv;
+  const int64_t hq = hkv * G;
+  const int64_t width = (hq + 2 * hkv) * kD;
+  const int64_t slot = pos >= 0 && pos < a.capacity ? pos : 0;
+  const bool is_q = lg < rows, is_k = lg == 8;
+  const int64_t head = is_q ? h * G + a.g0 + lg : is_k ? hq + h : hq + hkv + h;
+  PartialLoads L;
+  L.wv = load16<false>((is_q ? a.qw : a.kw) + 8 * r);
+  L.cv = load16<false>(a.cos + slot * kD + 8 * r);
+  L.sv = load16<false>(a.sin + slot * kD + 8 * r);
+  const float* p = static_cast<const float*>(a.qkv) + b * width + head * kD + 8 * r;
+#pragma unroll
+  for (int i = 0; i < kPrologueSplits; ++i) {
+    const int s = i < a.qkv_splits ? i : a.qkv_splits - 1;
+    const float4* q = reinterpret_cast<const float4*>(p + (int64_t)s * a.qkv_stride);
+    L.lo[i] = q[0];
+    L.hi[i] = q[1];
+  }
+  return L;
+}
+
+__device__ __forceinline__ uint4 partials_sum(const AttnArgs& a, const PartialLoads& L) {
+  float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kPrologueSplits; ++i) {
+    const bool on = i < a.qkv_splits;
+    y[0] = on ? y[0] + L.lo[i].x : y[0];
+    y[1] = on ? y[1] + L.lo[i].y : y[1];
+    y[2] = on ? y[2] + L.lo[i].z : y[2];
+    y[3] = on ? y[3] + L.lo[i].w : y[3];
+    y[4] = on ? y[4] + L.hi[i].x : y[4];
+    y[5] = on ? y[5] + L.hi[i].y : y[5];
+    y[6] = on ? y[6] + L.hi[i].z : y[6];
+    y[7] = on ? y[7] + L.hi[i].w : y[7];
+  }
+  return pack8(y);  // one rounding of the f32 sum
+}
+
 __device__ __forceinline__ bool prologue_finish(const AttnArgs& a, const PrologueLoads& L, int vh,
                                                 int lg, int r, int rows, int64_t start, int64_t pos,
                                                 uint4 (*qs)[16], uint4 (*kvs)[16]) {
@@ -519,10 +571,11 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
   const int64_t start = (int64_t)seg * a.span;
   int64_t end = start + a.span;
   if (end > used) end = used;
-  // The fused bf16-row path issues its first key blocks whether or not the
-  // wave has keys (their loads are discarded then); a head with no valid key
-  // at all reads them from the query gain (128 values, in bounds for every
-  // lane's offsets), so no cache slot at or beyond used is ever read.
+  // The fused paths with bf16 rows or up to kPrologueSplits partials issue
+  // their first key blocks whether or not the wave has keys (the loads are
+  // then discarded); a head with no valid key at all reads them from the
+  // query gain (128 values, in bounds for every lane's offsets), so no cache
+  // slot at or beyond used is ever read.
   const bool dummy = FUSED && used == 0;
   const uint16_t* kbase = dummy ? a.qw : a.k + (int64_t)vh * a.capacity * kD;
   const uint16_t* vbase = dummy ? a.qw : a.v + (int64_t)vh * a.capacity * kD;
@@ -565,6 +618,18 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
       const PrologueLoads pl = prologue_issue(a, vh, wave * 4 + q4, r, rows, pos);
 #pragma unroll
       for (int d = 0; d + 1 < NS; ++d) issue(d, d);
+      owns_slot = prologue_finish(a, pl, vh, wave * 4 + q4, r, rows, start, pos, qs, kvs);
+    } else if (a.qkv_splits <= kPrologueSplits) {
+      // split-K partials, likewise
+      const PartialLoads pp = partials_issue(a, vh, wave * 4 + q4, r, rows, pos);
+#pragma unroll
+      for (int d = 0; d + 1 < NS; ++d) issue(d, d);
+      __builtin_amdgcn_sched_barrier(0);  // every key load issued before the sum waits
+      PrologueLoads pl;
+      pl.wv = pp.wv;
+      pl.cv = pp.cv;
+      pl.sv = pp.sv;
+      pl.xv = partials_sum(a, pp);
       owns_slot = prologue_finish(a, pl, vh, wave * 4 + q4, r, rows, start, pos, qs, kvs);
     } else {
       if (n > 0) {

@@ -73,6 +73,7 @@ CASES = (  # b, hq, hk, cap, qkv splits, position, used rule
     (16, 32, 8, 641, 4, 640, "pos+1"),      # Qwen3-4B batch 16
     (1, 32, 8, 545, 0, 544, "pos+1"),       # Qwen3-4B batch 1 from bf16 rows (the folded step)
     (3, 6, 2, 257, 0, 63, "empty"),         # bf16 rows; mixed lengths and a head with no key
+    (2, 4, 2, 100, 3, 99, "empty"),         # the same from three split-K partials
 )
 
 
