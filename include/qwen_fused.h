@@ -425,6 +425,21 @@ int64_t qf_lm_head_blocks(int64_t vocab);
 int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const void* weight, int64_t vocab,
                       void* candidates, int64_t* tokens, void* logits, void* stream);
 
+/*
+ * qf_lm_head_argmax whose second launch also advances the decode state by one
+ * step, replacing the step's trailing `self.position.add_(1)`
+ * (engine/decode.py:107) and the attention lengths' increment:
+ *   position[0] += 1;  lengths[i] += 1 for i < length_count.
+ * position: int64 (8-byte aligned); lengths: int32 [length_count] (4-byte
+ * aligned; NULL when length_count is 0).  Nothing else in the call reads
+ * them.  Same errors as qf_lm_head_argmax, plus QF_E_ARG / QF_E_ALIGN for
+ * these two.
+ */
+int qf_lm_head_argmax_advance(const void* x, int64_t rows, int64_t k, const void* weight,
+                              int64_t vocab, void* candidates, int64_t* tokens, void* logits,
+                              int64_t* position, int32_t* lengths, int64_t length_count,
+                              void* stream);
+
 /* 8-byte candidate slots in qf_lm_head_argmax_static's scratch (8 MiB per GPU). */
 #define QF_LM_HEAD_STATIC_SLOTS (1 << 20)
 

@@ -845,9 +845,18 @@ int dispatch_silu(const SkinnyArgs& a, hipStream_t s) {
 // reduction order does not change the result.
 constexpr int kFinThreads = 1024;
 constexpr int kFinUnroll = 4;
+// With `position` set, workgroup 0 also advances the decode position and
+// the per-head lengths by one (the step's last writes, in the same launch).
 __global__ __launch_bounds__(kFinThreads) void argmax_finalize_kernel(const uint2* cand,
                                                                      int64_t blocks,
-                                                                     int64_t* tokens) {
+                                                                     int64_t* tokens,
+                                                                     int64_t* position,
+                                                                     int32_t* lengths,
+                                                                     int64_t length_count) {
+  if (position != nullptr && blockIdx.x == 0) {
+    if (threadIdx.x == 0) position[0] += 1;
+    for (int64_t i = threadIdx.x; i < length_count; i += kFinThreads) lengths[i] += 1;
+  }
   __shared__ float wv[kFinThreads / kWave];
   __shared__ int wi[kFinThreads / kWave];
   const int64_t row = blockIdx.x;
@@ -945,9 +954,11 @@ int lm_head_status(const void* x, int64_t rows, int64_t k, const void* weight, i
 }  // namespace
 }  // namespace qf
 
-extern "C" int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const void* weight,
-                                 int64_t vocab, void* candidates, int64_t* tokens, void* logits,
-                                 void* stream) {
+namespace {
+
+int lm_head_argmax(const void* x, int64_t rows, int64_t k, const void* weight, int64_t vocab,
+                   void* candidates, int64_t* tokens, void* logits, int64_t* position,
+                   int32_t* lengths, int64_t length_count, void* stream) {
   const int checked = lm_head_status(x, rows, k, weight, vocab, tokens, logits);
   if (checked != QF_OK) return checked;
   if (!candidates) return QF_E_ARG;
@@ -965,8 +976,30 @@ extern "C" int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const v
   const int st = dispatch_argmax(a, s);
   if (st != QF_OK) return st;
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)rows), dim3(kFinThreads), 0, s,
-                     static_cast<const uint2*>(candidates), vocab / kTile, tokens);
+                     static_cast<const uint2*>(candidates), vocab / kTile, tokens, position,
+                     lengths, length_count);
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" int qf_lm_head_argmax(const void* x, int64_t rows, int64_t k, const void* weight,
+                                 int64_t vocab, void* candidates, int64_t* tokens, void* logits,
+                                 void* stream) {
+  return lm_head_argmax(x, rows, k, weight, vocab, candidates, tokens, logits, nullptr, nullptr, 0,
+                        stream);
+}
+
+extern "C" int qf_lm_head_argmax_advance(const void* x, int64_t rows, int64_t k,
+                                         const void* weight, int64_t vocab, void* candidates,
+                                         int64_t* tokens, void* logits, int64_t* position,
+                                         int32_t* lengths, int64_t length_count, void* stream) {
+  if (!position || length_count < 0 || (length_count > 0 && !lengths)) return QF_E_ARG;
+  if ((reinterpret_cast<uintptr_t>(position) & 7u) != 0 ||
+      (reinterpret_cast<uintptr_t>(lengths) & 3u) != 0)
+    return QF_E_ALIGN;
+  return lm_head_argmax(x, rows, k, weight, vocab, candidates, tokens, logits, position, lengths,
+                        length_count, stream);
 }
 
 // Candidate scratch of qf_lm_head_argmax_static: a file-scope device array,

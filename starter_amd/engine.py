@@ -318,16 +318,18 @@ class Engine:
             return linear_silu_mul(normed, gate_up)
         return silu_mul(F.linear(normed, gate_up))
 
-    def _select(self, normed, tokens):
+    def _select(self, normed, tokens, advance=None):
         """LM head + greedy choice: writes the tokens; returns the bf16 logits
-        when ``keep_logits`` (else None)."""
+        when ``keep_logits`` (else None) and whether the fused LM head also
+        advanced ``advance`` = (position, lengths) by one (the step's last
+        writes, without two more launches)."""
         if _lm_head.supports(normed, self.lm_head):
             out = _lm_head.lm_head_argmax(normed, self.lm_head, logits=self.keep_logits,
-                                          tokens=tokens)
-            return out[1] if self.keep_logits else None
+                                          tokens=tokens, advance=advance)
+            return (out[1] if self.keep_logits else None), advance is not None
         logits = F.linear(normed, self.lm_head)
         tokens.copy_(logits.argmax(-1))
-        return logits
+        return logits, False
 
     def _next_norm(self, index):
         if index + 1 < len(self.layers):
@@ -374,7 +376,7 @@ class Engine:
                 x = x.view(batch, length, -1)[:, -1].contiguous()
                 hidden = hidden.view(batch, length, -1)[:, -1].contiguous()
             x, normed = add_rms_norm(x, F.linear(hidden, layer.down), weight, eps)
-        return self._select(normed, st.tokens)
+        return self._select(normed, st.tokens)[0]
 
     def _run_prefill(self, st: _State):
         """Prefill from a HIP graph captured on the first prompt of this shape
@@ -446,9 +448,10 @@ class Engine:
                 weight, eps = self._next_norm(index)
                 x, normed = add_rms_norm(x, self._project(hidden, layer.down), weight, eps)
                 sq = None
-        logits = self._select(normed, st.tokens)
-        st.position.add_(1)
-        st.used.add_(1)
+        logits, advanced = self._select(normed, st.tokens, (st.position, st.used))
+        if not advanced:
+            st.position.add_(1)
+            st.used.add_(1)
         return logits
 
     def _capture(self, st: _State):

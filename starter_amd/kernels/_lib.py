@@ -66,6 +66,8 @@ SIGNATURES = {
                                 _i32),
     "qf_lm_head_blocks": ([_i64], _i64),
     "qf_lm_head_argmax": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp], _i32),
+    "qf_lm_head_argmax_advance": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp],
+                                  _i32),
     "qf_lm_head_argmax_static": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp], _i32),
 }
 

@@ -29,10 +29,12 @@ def supports(x, weight) -> bool:
             and x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
 
 
-def lm_head_argmax(x, weight, logits: bool = False, tokens=None):
+def lm_head_argmax(x, weight, logits: bool = False, tokens=None, advance=None):
     """Greedy tokens int64 [M] of bf16 logits x @ weight.T; with ``logits=True``
     also returns those bf16 logits [M, V].  ``tokens`` may be a contiguous
-    int64 [M] tensor on x's device to write the tokens into."""
+    int64 [M] tensor on x's device to write the tokens into.  ``advance``:
+    optional (position int64 [1], lengths int32 [L]) device tensors that the
+    same launches increment by one (the decode step's state advance)."""
     if not supports(x, weight):
         raise ValueError("expected contiguous BF16 CUDA x[M<=64,K], W[V,K] with K % 64 == 0, V % 16 == 0")
     rows, k = x.shape
@@ -45,6 +47,17 @@ def lm_head_argmax(x, weight, logits: bool = False, tokens=None):
           or not tokens.is_contiguous()):
         raise ValueError("tokens must be a contiguous int64 [M] tensor on x's device")
     out = torch.empty((rows, vocab), dtype=torch.bfloat16, device=x.device) if logits else None
-    _lib.call("qf_lm_head_argmax", x.data_ptr(), rows, k, weight.data_ptr(), vocab,
-              candidates.data_ptr(), tokens.data_ptr(), _lib.ptr(out), _lib.stream(x.device))
+    if advance is None:
+        _lib.call("qf_lm_head_argmax", x.data_ptr(), rows, k, weight.data_ptr(), vocab,
+                  candidates.data_ptr(), tokens.data_ptr(), _lib.ptr(out), _lib.stream(x.device))
+    else:
+        position, lengths = advance
+        for t, dtype in ((position, torch.int64), (lengths, torch.int32)):
+            if t.dtype != dtype or t.device != x.device or not t.is_contiguous():
+                raise ValueError("advance takes contiguous int64 position and int32 lengths on x's device")
+        if position.numel() != 1:
+            raise ValueError("position must hold one element")
+        _lib.call("qf_lm_head_argmax_advance", x.data_ptr(), rows, k, weight.data_ptr(), vocab,
+                  candidates.data_ptr(), tokens.data_ptr(), _lib.ptr(out), position.data_ptr(),
+                  lengths.data_ptr(), lengths.numel(), _lib.stream(x.device))
     return (tokens, out) if logits else tokens

@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 31
+    assert len(names) == 32
 
 
 def test_library_exports_every_symbol():
@@ -100,6 +100,11 @@ def test_host_side_argument_errors_launch_nothing():
     assert lib.qf_lm_head_argmax(bogus, 1, 2560, bogus, 151930, bogus, bogus, None, None) == -2
     assert lib.qf_lm_head_argmax(bogus, 1, 2560, bogus, 151936, None, bogus, None, None) == -1
     assert lib.qf_lm_head_argmax(bogus + 8, 1, 2560, bogus, 151936, bogus, bogus, None, None) == -3
+    adv = lib.qf_lm_head_argmax_advance
+    assert adv(bogus, 1, 2560, bogus, 151936, bogus, bogus, None, None, None, 0, None) == -1
+    assert adv(bogus, 1, 2560, bogus, 151936, bogus, bogus, None, bogus, None, 8, None) == -1
+    assert adv(bogus, 1, 2560, bogus, 151936, bogus, bogus, None, bogus + 4, bogus, 8, None) == -3
+    assert adv(bogus, 65, 2560, bogus, 151936, bogus, bogus, None, bogus, bogus, 8, None) == -2
     pa = lib.qf_prefill_attention
     assert pa(bogus, bogus, bogus, 1, 0, 32, 8, 64, 0.1, bogus, None) == -1       # empty prompt
     assert pa(bogus, bogus, bogus, 1, 65, 32, 8, 64, 0.1, bogus, None) == -1      # past capacity

@@ -92,3 +92,37 @@ def test_graph_replay_follows_fresh_inputs():
         eager_tokens, eager_logits = lm_head_argmax(x, w, logits=True)
         assert torch.equal(tokens, eager_tokens) and torch.equal(logits, eager_logits)
         assert torch.equal(tokens, logits.argmax(-1))
+
+
+def test_advance_entry_matches_and_advances():
+    """qf_lm_head_argmax_advance: the same tokens and logits as the plain
+    entry, and the position and every length one higher afterwards (the
+    decode step's state advance in the same launches), also in a replayed
+    graph."""
+    g = torch.Generator(device="cuda").manual_seed(91)
+    x = torch.randn(3, 512, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(4096, 512, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+    want_tokens, want_logits = lm_head_argmax(x, w, logits=True)
+    position = torch.tensor([41], dtype=torch.int64, device="cuda")
+    lengths = torch.arange(24, dtype=torch.int32, device="cuda") * 7
+    start_len = lengths.clone()
+    tokens, logits = lm_head_argmax(x, w, logits=True, advance=(position, lengths))
+    torch.cuda.synchronize()
+    assert torch.equal(tokens, want_tokens) and torch.equal(logits, want_logits)
+    assert position.item() == 42 and torch.equal(lengths, start_len + 1)
+    out = torch.empty(3, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        lm_head_argmax(x, w, tokens=out, advance=(position, lengths))
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        lm_head_argmax(x, w, tokens=out, advance=(position, lengths))
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want_tokens)
+    assert position.item() == 46 and torch.equal(lengths, start_len + 5)
+    with pytest.raises(ValueError):
+        lm_head_argmax(x, w, advance=(position.to(torch.int32), lengths))
