@@ -16,7 +16,10 @@
  *   - Return value: 0 on success; a negative QF_E* code for an argument error
  *     detected on the host before anything is launched; otherwise the positive
  *     hipError_t reported for the launch.  qf_error_string() names a code.
- *   - The library keeps no mutable global state; calls are reentrant.
+ *   - The library keeps no mutable global state, with one exception:
+ *     qf_lm_head_argmax_static's per-GPU static scratch array (and the host
+ *     cache of its device addresses, guarded by a mutex).  Every other call
+ *     is reentrant.
  *   - Inputs are read-only.  Outputs must not alias inputs.
  *
  * Each entry point cites the reference (jadenpxrk/starter) Python/Triton
@@ -454,8 +457,11 @@ int qf_lm_head_argmax_advance(const void* x, int64_t rows, int64_t k, const void
  * rows * qf_lm_head_blocks(vocab) exceeds QF_LM_HEAD_STATIC_SLOTS (64 rows
  * of a vocabulary up to 262,144).  Calls that overlap on one GPU (other
  * streams or threads) share the array and race: order them on one stream.
- * The first call on a device looks the array's address up (a host call,
- * no allocation) and keeps it.
+ * The array used is the one on the device `stream` belongs to (the current
+ * device for the null stream).  The first call on a device looks its address
+ * up (a host call, no allocation; briefly making that device current if it
+ * is not) and keeps it, so a call under graph capture that is the first on
+ * its device still captures only kernel launches.
  */
 int qf_lm_head_argmax_static(const void* x, int64_t rows, int64_t k, const void* weight,
                              int64_t vocab, int64_t* tokens, void* logits, void* stream);

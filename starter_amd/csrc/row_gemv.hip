@@ -11,14 +11,19 @@
 //
 // * residual epilogue (qf_linear_residual, qf_linear_residual_merged):
 //     y = bf16(x W^T);  total = bf16(residual + y)
-//   and per workgroup g the f64 sum of total^2 over its columns,
-//   sq[r][g] (exact: squares of bf16 values, at most 16 significant bits).
+//   and per workgroup g the f64 sum of total^2 over its columns, sq[r][g]
+//   (squares of bf16 values have at most 16 significant bits, so the sums
+//   are exact while a row's squares span less than about 53 - 16 - log2(k)
+//   bits of exponent).
 // * normalising prologue (qf_linear_normed, qf_linear_silu_mul_normed):
 //     inv = 1 / sqrt(f32(sum_g sq[r][g]) / k + eps)
 //     x   = bf16(bf16(total * inv) * gain);  out = bf16(x W^T)
 //   with the same rounding steps as qf_add_rms_norm, so x is bit-identical
-//   to the normalised row that launch would have written (the f64 sum is
-//   exact, so its order does not matter).
+//   to the normalised row that launch would have written whenever the f64
+//   sums are exact.  Rows with a wider spread (Qwen3's massive activations
+//   next to near-zero values) add their squares in a different order from
+//   qf_add_rms_norm; the two totals then differ by far less than an f32 ulp
+//   and round to the same f32 except in rare near-tie cases.
 //
 // Two more ends complete a decoder layer: the SiLU * up epilogue of the
 // packed gate/up projection (bf16(bf16(silu(bf16(g))) * bf16(u)), as

@@ -1014,10 +1014,15 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch[kMaxDevices] = {};
 
-// This device's address of `scratch` (nullptr and a status on failure).
-void* scratch_address(int* status) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+// The address of `scratch` on the device `stream` belongs to (the current
+// device for the null stream); nullptr and a status on failure.  The lookup
+// runs with that device current - hipGetSymbolAddress answers for the current
+// device - and the caller's current device is restored afterwards.
+void* scratch_address(hipStream_t stream, int* status) {
+  int current = 0;
+  hipError_t e = hipGetDevice(&current);
+  int dev = current;
+  if (e == hipSuccess && stream != nullptr) e = hipStreamGetDevice(stream, &dev);
   if (e != hipSuccess) {
     *status = static_cast<int>(e);
     return nullptr;
@@ -1028,8 +1033,14 @@ void* scratch_address(int* status) {
   }
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch[dev] == nullptr) {
+    if (dev != current && (e = hipSetDevice(dev)) != hipSuccess) {
+      *status = static_cast<int>(e);
+      return nullptr;
+    }
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    const hipError_t restored = dev != current ? hipSetDevice(current) : hipSuccess;
+    if (e == hipSuccess) e = restored;
     if (e != hipSuccess || ptr == nullptr) {
       *status = e != hipSuccess ? static_cast<int>(e) : QF_E_ARG;
       return nullptr;
@@ -1048,7 +1059,7 @@ extern "C" int qf_lm_head_argmax_static(const void* x, int64_t rows, int64_t k,
   if (checked != QF_OK) return checked;
   if (rows * (vocab / kTile) > QF_LM_HEAD_STATIC_SLOTS) return QF_E_CAPACITY;
   int status = QF_OK;
-  void* candidates = scratch_address(&status);
+  void* candidates = scratch_address(static_cast<hipStream_t>(stream), &status);
   if (candidates == nullptr) return status;
   // Every candidate slot the finalize kernel reads is written first by the
   // projection's epilogue, so nothing left by an earlier call is read.

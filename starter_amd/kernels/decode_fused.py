@@ -25,15 +25,18 @@ def _next_power_of_2(n: int) -> int:
 
 
 def _rows(x):
-    """Shape of a contiguous 2-D BF16 CUDA tensor (engine/kernels/decode_fused.py:121-124)."""
+    """(rows, cols) of ``x``, which must be a dense 2-D bf16 tensor on a GPU;
+    anything else raises ValueError (engine/kernels/decode_fused.py:121-124)."""
     if x.ndim != 2 or not x.is_cuda or x.dtype != torch.bfloat16 or not x.is_contiguous():
         raise ValueError("expected a contiguous 2-D BF16 CUDA tensor")
     return x.shape
 
 
 def _splits(branch, shape, device):
-    """0 for a BF16 [rows, cols] operand; S for FP32 split-K partials [S, rows, cols]
-    (engine/kernels/decode_fused.py:127-137)."""
+    """How the kernel reads ``branch``: 0 when it is a bf16 matrix shaped like
+    the residual, or the split count S when it is a dense f32 stack of S
+    split-K partial products ``[S, rows, cols]``; any other operand raises
+    ValueError (engine/kernels/decode_fused.py:127-137)."""
     if branch.ndim == 3 and branch.dtype == torch.float32:
         if (tuple(branch.shape[1:]) != tuple(shape) or branch.shape[0] < 1
                 or branch.device != device or not branch.is_contiguous()):
@@ -46,11 +49,15 @@ def _splits(branch, shape, device):
 
 
 def add_rms_norm(residual, branch, weight, eps):
-    """Return (residual + branch, RMSNorm of that sum); fresh [rows, cols] BF16 tensors.
+    """One launch for the two steps between sublayers: ``total`` = bf16 sum of
+    the residual stream and the sublayer's output ``branch``, and ``normed``
+    = RMSNorm of ``total`` with gain ``weight``; both are new bf16 tensors
+    shaped like ``residual``, which is left as it was.
 
-    ``branch`` is BF16 [rows, cols], or FP32 split-K partials [S, rows, cols]
-    that are added in split order and rounded once to BF16 inside the kernel.
-    Mirrors engine/kernels/decode_fused.py:140-158.
+    A bf16 ``branch`` is added as is.  An f32 ``branch`` holds a projection's
+    S split-K partials: the kernel sums them from split 0 upwards in f32 and
+    rounds that sum to bf16 once before the add
+    (engine/kernels/decode_fused.py:140-158 is the function this replaces).
     """
     n_rows, n_cols = _rows(residual)
     if tuple(weight.shape) != (n_cols,):
@@ -70,10 +77,12 @@ def add_rms_norm(residual, branch, weight, eps):
 
 
 def silu_mul(gate_up, block=1024):
-    """silu(gate) * up for a packed [rows, 2 * cols] projection; returns [rows, cols].
+    """The MLP activation on a packed gate/up projection: row r of the
+    ``[rows, 2N]`` input holds the N gate values, then the N up values; the
+    new ``[rows, N]`` bf16 output holds bf16(bf16(SiLU(gate)) * up).
 
-    ``block`` is accepted for signature compatibility with
-    engine/kernels/decode_fused.py:161; the HIP kernel chooses its own tiling.
+    ``block`` exists so calls written for engine/kernels/decode_fused.py:161
+    still bind; the HIP kernel picks its own tiling and ignores it.
     """
     n_rows, width = _rows(gate_up)
     if width % 2:

@@ -50,12 +50,13 @@ def _row_walk(x: torch.Tensor):
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """RMSNorm over the last dimension, matching ``Qwen3RMSNorm.forward``.
+    """Normalise every length-C row of ``x`` (C = ``weight.numel()``, its last
+    dimension) by the root mean square of its f32 values, then apply the
+    bf16 gain ``weight`` - the arithmetic and rounding of Qwen3RMSNorm.
 
-    ``x`` is any shape whose last dimension matches ``weight``; ``weight`` is
-    the module's learned gain, in the same dtype as ``x`` (bf16).  Returns a
-    fresh contiguous tensor of ``x``'s shape.  Mirrors
-    engine/kernels/rmsnorm.py:39-62.
+    Both operands are bf16 on one GPU; ``x`` may be a strided view.  The
+    result is a new contiguous tensor shaped like ``x``
+    (engine/kernels/rmsnorm.py:39-62 is the function this replaces).
     """
     shape = x.shape
     if x.ndim == 0:

@@ -44,12 +44,18 @@ def partition_keys(virtual_heads, capacity, multiprocessors):
 
 
 class SmallQueryAttention:
-    """Fixed-shape, read-only attention; returns fresh [B,1,Hq,128] BF16 output.
+    """Decode attention for one shape, fixed at construction (batch, query and
+    key/value heads, cache capacity): each call attends B one-token queries
+    over the first ``used`` keys of their K/V cache rows and writes a new bf16
+    ``[B, 1, Hq, 128]`` result; the caches are only read.
 
-    USED is contiguous int32 [B*Hkv], with 0 <= each value <= capacity.
-    Calls must be ordered on one stream; concurrent calls cannot share this
-    instance (its f32 scratch holds the per-segment partials).  Mirrors
-    engine/kernels/small_query_attention.py:113-158.
+    ``used`` is a dense int32 vector of B*Hkv key counts, each in
+    [0, capacity], one per (sequence, key/value head).  The instance owns
+    the f32 buffers its key segments merge through, so two calls in flight
+    at once (other streams or threads) would overwrite each other's
+    partials: issue them on one stream
+    (engine/kernels/small_query_attention.py:113-158 is the class this
+    replaces).
     """
 
     def __init__(self, batch, query_heads, kv_heads, capacity, device):

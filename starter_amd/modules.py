@@ -16,6 +16,8 @@
 
 from __future__ import annotations
 
+import copy
+
 import torch
 from torch import nn
 from torch.nn import functional as F
@@ -23,6 +25,7 @@ from torch.nn import functional as F
 from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 from transformers.models.qwen3.modeling_qwen3 import Qwen3Attention, eager_attention_forward
 
+from .engine import _pack_rows
 from .kernels.decode_fused import silu_mul
 from .kernels.embedding import FusedEmbedding
 from .kernels.qk_norm_rope import HEAD, qk_norm_rope
@@ -69,30 +72,24 @@ class PackedMLP(nn.Module):
 class DecodeQKNormRoPE(Qwen3Attention):
     """``Qwen3Attention`` with the decode-step Q/K norm + RoPE fused.
 
-    Shares every submodule and attribute of the attention it wraps (no weight
-    is allocated or initialised), and packs the three input projections into
-    one ``qkv_weight`` ``[(Hq + 2 Hkv) * 128, H]`` whose row ranges become the
-    q/k/v modules' weights, so the state dict and the prefill path read the
-    same storage as the packed decode step (engine/qk_norm_rope.py:11-30).
+    Adopts the wrapped attention's whole instance state - its submodules,
+    parameters, buffers and configuration attributes, whatever this
+    transformers version gives a ``Qwen3Attention`` - so no weight is
+    allocated or initialised.  The q, k and v projections are then packed
+    into one ``qkv_weight`` ``[(Hq + 2 Hkv) * 128, H]`` by the engine's own
+    row packer, so the three modules read row ranges of it and the state dict,
+    the prefill path and the fused decode step share one copy
+    (engine/qk_norm_rope.py:10-30).
     """
-
-    _COPIED = ("config", "layer_idx", "layer_type", "head_dim", "num_key_value_groups",
-               "scaling", "attention_dropout", "is_causal", "sliding_window", "q_proj",
-               "k_proj", "v_proj", "o_proj", "q_norm", "k_norm")
 
     @torch.no_grad()
     def __init__(self, reference):
         nn.Module.__init__(self)
-        for name in self._COPIED:
-            if hasattr(reference, name):
-                setattr(self, name, getattr(reference, name))
-        self.train(reference.training)
-        self.qkv_weight = torch.cat((self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
-        start = 0
-        for module in (self.q_proj, self.k_proj, self.v_proj):
-            stop = start + module.weight.shape[0]
-            module.weight = nn.Parameter(self.qkv_weight[start:stop], requires_grad=False)
-            start = stop
+        # new containers, same members: swapping a module on one adapter does
+        # not reach back into the wrapped attention
+        for key, value in vars(reference).items():
+            self.__dict__[key] = copy.copy(value) if isinstance(value, dict) else value
+        self.qkv_weight = _pack_rows(self.q_proj, self.k_proj, self.v_proj)
 
     def _fused(self, hidden_states, cos, sin, cache, kwargs) -> bool:
         """True when the one-token kernel applies.  Reads shapes, dtypes and
@@ -133,7 +130,11 @@ class DecodeQKNormRoPE(Qwen3Attention):
         q, k = qk_norm_rope(q, k, self.q_norm.weight, self.k_norm.weight, cos, sin,
                             self.q_norm.variance_epsilon, self.k_norm.variance_epsilon)
         if past_key_values is not None:
-            k, v = past_key_values.update(k, v, self.layer_idx)
+            # transformers 4.x's StaticCache writes the slots named by
+            # cache_position and, without it, every slot (engine/qk_norm_rope.py:
+            # 64-66 passes the same three); transformers 5 layers ignore them
+            k, v = past_key_values.update(k, v, self.layer_idx, {
+                "sin": sin, "cos": cos, "cache_position": kwargs.get("cache_position")})
         interface = ALL_ATTENTION_FUNCTIONS.get_interface(self.config._attn_implementation,
                                                           eager_attention_forward)
         output, weights = interface(self, q, k, v, attention_mask, dropout=0.0,

@@ -88,3 +88,44 @@ def test_single_token_attention_matches_native_module(models):
                              (ours.layers[0].values, theirs.layers[0].values)):
         assert ours_t.shape[2] == theirs_t.shape[2] == 10
         torch.testing.assert_close(ours_t[:, :, -1], theirs_t[:, :, -1], rtol=0.02, atol=0.02)
+
+
+@torch.inference_mode()
+def test_decode_through_static_cache_matches_native(models):
+    """The fixed-capacity cache the reference engine decodes into
+    (engine/decode.py:7-12, a StaticCache subclass): four greedy steps after
+    a 6-token prompt, and every one-token ``update`` receives the rotary rows
+    and ``cache_position`` the reference adapter hands it
+    (engine/qk_norm_rope.py:64-66) - transformers 4.x's static layer writes
+    the slots ``cache_position`` names."""
+    from transformers import StaticCache
+
+    native, candidate = models
+    torch.manual_seed(5)
+    prompt = torch.randint(0, 127, (2, 6), device="cuda")
+    ours = StaticCache(config=candidate.config, max_cache_len=16)
+    theirs = StaticCache(config=native.config, max_cache_len=16)
+    seen = []
+    real_update = ours.update
+
+    def update(key, value, layer_idx, cache_kwargs=None):
+        seen.append(cache_kwargs)
+        return real_update(key, value, layer_idx, cache_kwargs)
+
+    ours.update = update
+    current, start = prompt, 0
+    for step in range(4):
+        position = torch.arange(start, start + current.shape[1], device="cuda")
+        seen.clear()
+        actual = candidate(input_ids=current, past_key_values=ours, use_cache=True,
+                           cache_position=position, logits_to_keep=1).logits
+        expected = native(input_ids=current, past_key_values=theirs, use_cache=True,
+                          cache_position=position, logits_to_keep=1).logits
+        torch.testing.assert_close(actual, expected, rtol=0.03, atol=0.04)
+        if current.shape[1] == 1:
+            assert len(seen) == len(candidate.model.layers)
+            for kwargs in seen:
+                assert set(kwargs) == {"sin", "cos", "cache_position"}
+                assert torch.equal(kwargs["cache_position"], position)
+        start += current.shape[1]
+        current = actual[:, -1].argmax(-1, keepdim=True)

@@ -90,3 +90,77 @@ def test_capacity_refused_before_launch():
     assert b"static scratch" in lib.qf_error_string(st)
     torch.cuda.synchronize()
     assert bool((tokens == -7).all())
+
+
+def _graph_replays_match(x, w, replays=3):
+    """Capture qf_lm_head_argmax_static in a HIP graph (torch.cuda.graph), then
+    replay it several times with eager work and synchronisations between the
+    replays, each replay against qf_lm_head_argmax run eagerly."""
+    lib = _lib.lib()
+    rows, k = x.shape
+    vocab = w.shape[0]
+    tokens = torch.full((rows,), -7, dtype=torch.int64, device=DEV)
+    logits = torch.full((rows, vocab), float("nan"), dtype=torch.bfloat16, device=DEV)
+    graph = torch.cuda.graph_pool_handle()
+    g = torch.cuda.CUDAGraph()
+    status = []
+    with torch.cuda.graph(g, pool=graph):
+        status.append(lib.qf_lm_head_argmax_static(
+            x.data_ptr(), rows, k, w.data_ptr(), vocab, tokens.data_ptr(), logits.data_ptr(),
+            _lib.stream(x.device)))
+    assert status == [0], lib.qf_error_string(status[0])
+    cand = torch.empty((rows, lib.qf_lm_head_blocks(vocab), 2), dtype=torch.int32, device=DEV)
+    for replay in range(replays):
+        x.mul_(-1 if replay % 2 else 1)          # eager work between replays
+        tokens.fill_(-7)
+        logits.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        want_tokens = torch.empty_like(tokens)
+        want_logits = torch.empty_like(logits)
+        st = lib.qf_lm_head_argmax(x.data_ptr(), rows, k, w.data_ptr(), vocab, cand.data_ptr(),
+                                   want_tokens.data_ptr(), want_logits.data_ptr(),
+                                   _lib.stream(x.device))
+        assert st == 0, lib.qf_error_string(st)
+        torch.cuda.synchronize()
+        assert torch.equal(tokens, want_tokens), replay
+        assert_bits_exact(logits, want_logits, what=f"replay {replay}")
+
+
+def test_static_entry_replays_in_a_graph():
+    g = gen(903)
+    _graph_replays_match(normal((4, 2560), g=g).to(DEV), normal((32768, 2560), 0.0, 0.02, g).to(DEV))
+
+
+_FIRST_CALL_CAPTURED = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
+import test_zz_no_alloc as t
+from conftest import gen, normal
+g = gen(904)
+x = normal((2, 1024), g=g).to("cuda")
+w = normal((8192, 1024), 0.0, 0.02, g).to("cuda")
+# the library's kernels are loaded by an eager call of another entry point;
+# the static entry's first call - its address lookup - happens under capture
+lib = t._lib.lib()
+cand = torch.empty((2, lib.qf_lm_head_blocks(8192), 2), dtype=torch.int32, device="cuda")
+tok = torch.empty(2, dtype=torch.int64, device="cuda")
+assert lib.qf_lm_head_argmax(x.data_ptr(), 2, 1024, w.data_ptr(), 8192, cand.data_ptr(),
+                             tok.data_ptr(), None, t._lib.stream(x.device)) == 0
+torch.cuda.synchronize()
+t._graph_replays_match(x, w)
+print("first-call-under-capture ok", flush=True)
+"""
+
+
+def test_static_entry_first_call_under_capture():
+    """In a fresh process the first call of the static entry on the device -
+    the one that looks the scratch address up - is made under capture."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    out = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, str(root)],
+                         capture_output=True, text=True, timeout=240)
+    assert out.returncode == 0, out.stdout[-2000:] + out.stderr[-4000:]
+    assert "first-call-under-capture ok" in out.stdout
