@@ -10,6 +10,12 @@ Every source is compiled for gfx950 only, with:
   warning is harmless);
 * HIP's default correctly rounded f32 divide and sqrt.
 
+A second library, ``starter_amd/kernels/libqwen_fused_phases.so``, holds only
+the decode attention built with ``-DQF_PHASE_STAMPS``: the same kernels plus
+an instrumented entry point that records per-workgroup phase timestamps
+(``starter_amd.attention_phases`` reads them).  Nothing in the product loads
+it.
+
 Run ``python -m starter_amd.build`` or call :func:`build`.
 """
 
@@ -27,6 +33,8 @@ ROOT = PACKAGE.parent
 CSRC = PACKAGE / "csrc"
 OBJ_DIR = PACKAGE / "_build"
 LIBRARY = PACKAGE / "kernels" / "libqwen_fused.so"
+PHASES_LIBRARY = PACKAGE / "kernels" / "libqwen_fused_phases.so"
+PHASES_SOURCE = "decode_attention.hip"
 SOURCES = ("rmsnorm.hip", "silu_mul.hip", "qk_norm_rope.hip", "embedding.hip", "skinny_gemm.hip",
            "decode_attention.hip", "prefill_attention.hip", "row_gemv.hip")
 ARCH = "gfx950"
@@ -73,7 +81,8 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile every HIP source and link the shared library; return its path."""
+    """Compile every HIP source and link the shared library (and the phase
+    timing library); return the product library's path."""
     cc = hipcc()
     OBJ_DIR.mkdir(exist_ok=True)
     jobs = []
@@ -81,14 +90,19 @@ def build(verbose: bool = False) -> Path:
         obj = OBJ_DIR / (Path(name).stem + ".o")
         jobs.append((obj, [cc, *COMPILE_FLAGS, *EXTRA_FLAGS.get(name, ()), "-c", str(CSRC / name),
                            "-o", str(obj)]))
-    workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
+    phases_obj = OBJ_DIR / (Path(PHASES_SOURCE).stem + "_phases.o")
+    phases_job = (phases_obj, [cc, *COMPILE_FLAGS, *EXTRA_FLAGS.get(PHASES_SOURCE, ()),
+                               "-DQF_PHASE_STAMPS", "-c", str(CSRC / PHASES_SOURCE),
+                               "-o", str(phases_obj)])
+    workers = min(len(jobs) + 1, max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
-        for fut in [pool.submit(_run, cmd, verbose) for _, cmd in jobs]:
+        for fut in [pool.submit(_run, cmd, verbose) for _, cmd in (*jobs, phases_job)]:
             fut.result()
-    tmp = LIBRARY.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-          *[str(obj) for obj, _ in jobs]], verbose)
-    os.replace(tmp, LIBRARY)
+    for library, objects in ((LIBRARY, [obj for obj, _ in jobs]), (PHASES_LIBRARY, [phases_obj])):
+        tmp = library.with_suffix(".so.tmp")
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+              *[str(obj) for obj in objects]], verbose)
+        os.replace(tmp, library)
     return LIBRARY
 
 

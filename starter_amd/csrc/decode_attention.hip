@@ -73,7 +73,25 @@ struct AttnArgs {
   const int64_t* position;
   uint16_t* kc;
   uint16_t* vc;
+  // Phase timestamps (the instrumented build only; see kPhases).
+  uint64_t* stamps;
 };
+
+// Phase boundaries an instrumented attention workgroup records
+// (s_memrealtime: the constant clock, one time base for every CU).  Wave 0:
+//   0 entry; 1 `used` and the position have arrived; 2 the fused prologue's
+//   loads (and the first key blocks behind them) are issued; 3 the queries
+//   are normalised, rotated and in every wave (after the barrier); 4 the
+//   wave's first key block is consumed (its loads landed, scores, softmax
+//   and P V done); 5 the key loop is done; 6 the four waves are merged;
+//   7 the output or partials are stored and acknowledged; 12 every wave has
+//   passed the barrier before the merge.
+// Wave w: 8 + w its key loop done; 12 + w (w > 0) its first block consumed.
+// The merge kernel records 0 entry, 1 merged, 2 stored and acknowledged.
+constexpr int kPhases = 16;
+constexpr int kMergePhases = 4;
+
+__device__ __forceinline__ uint64_t phase_clock() { return __builtin_amdgcn_s_memrealtime(); }
 
 __device__ __forceinline__ float dpp_f32_sum16(float x) {
   // All-reduce over aligned 16-lane rows (every lane ends with the sum).
@@ -546,9 +564,19 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 constexpr int kVRow = 288;  // LDS bytes per staged V key row (256 + 32 pad)
 
-template <int GT, bool FUSED, bool NTL = false, int NS = 2>
+// Where the query rows come from (attn_mfma_kernel's PRO): q in memory, or
+// the fused Q/K/V prologue over bf16 rows, over at most kPrologueSplits f32
+// split-K partials, or over more partials.  One kernel per source keeps each
+// prologue straight-line code, so the compiler's wait counts see exactly the
+// loads of one path.
+constexpr int kProNone = 0, kProRows = 1, kProPartials = 2, kProMany = 3;
+
+template <int GT, int PRO, bool NTL = false, int NS = 2, bool STAMP = false>
 __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
   static_assert(GT == 1 || GT == 2 || GT == 4, "query rows per kv head");
+  constexpr bool FUSED = PRO != kProNone;
+  uint64_t ts[kPhases] = {};
+  if constexpr (STAMP) ts[0] = phase_clock();
   constexpr int kW = kBlock / kWave;
   __shared__ float xm[kW][GT], xl[kW][GT];
   __shared__ float xacc[kW][GT][kD];
@@ -557,7 +585,7 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
   const int vh = blockIdx.x;
   const int seg = blockIdx.y;
   const int lane = threadIdx.x % kWave;
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: scalar branches
   const int r = lane % 16;
   const int q4 = lane / 16;
   const int G = a.groups;  // <= GT
@@ -566,6 +594,10 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
   const int32_t used_in = a.used[vh];
   const int64_t pos_in = FUSED ? *a.position : 0;
   if constexpr (FUSED) asm volatile("" ::"s"(used_in), "s"(pos_in));
+  if constexpr (STAMP) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::"s"(used_in), "s"(pos_in) : "memory");
+    ts[1] = phase_clock();
+  }
   int64_t used = used_in;
   used = used < 0 ? 0 : (used > a.capacity ? a.capacity : used);
   const int64_t start = (int64_t)seg * a.span;
@@ -610,35 +642,49 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
   };
   if constexpr (FUSED) {
     pos = pos_in;
-    bool owns_slot;
-    if (a.qkv_splits == 0) {
+    // Only waves 0 and 1 hold a prologue row: wave 0's lane groups the query
+    // rows (lane group q4 < rows), wave 1's lane groups 8 (the new key) and
+    // 9 (the new value); waves 2 and 3 issue nothing but their key blocks
+    // (the prologue's loads from all four waves took 1.8 us to issue with
+    // eight split-K partials, measured with the phase stamps).
+    const bool pro = wave < 2;
+    const int plg = wave == 0 ? q4 : 8 + q4;
+    const bool owns_slot = pos >= 0 && pos < a.capacity && pos >= start && pos < start + a.span;
+    if constexpr (PRO == kProRows) {
       // bf16 rows: the prologue's loads, then the first key blocks (issued
       // unconditionally, so the prologue waits for its own loads only and
       // its arithmetic overlaps the key loads).
-      const PrologueLoads pl = prologue_issue(a, vh, wave * 4 + q4, r, rows, pos);
+      PrologueLoads pl;
+      if (pro) pl = prologue_issue(a, vh, plg, r, rows, pos);
 #pragma unroll
       for (int d = 0; d + 1 < NS; ++d) issue(d, d);
-      owns_slot = prologue_finish(a, pl, vh, wave * 4 + q4, r, rows, start, pos, qs, kvs);
-    } else if (a.qkv_splits <= kPrologueSplits) {
+      if constexpr (STAMP) ts[2] = phase_clock();
+      if (pro) prologue_finish(a, pl, vh, plg, r, rows, start, pos, qs, kvs);
+    } else if constexpr (PRO == kProPartials) {
       // split-K partials, likewise
-      const PartialLoads pp = partials_issue(a, vh, wave * 4 + q4, r, rows, pos);
+      PartialLoads pp;
+      if (pro) pp = partials_issue(a, vh, plg, r, rows, pos);
 #pragma unroll
       for (int d = 0; d + 1 < NS; ++d) issue(d, d);
       __builtin_amdgcn_sched_barrier(0);  // every key load issued before the sum waits
-      PrologueLoads pl;
-      pl.wv = pp.wv;
-      pl.cv = pp.cv;
-      pl.sv = pp.sv;
-      pl.xv = partials_sum(a, pp);
-      owns_slot = prologue_finish(a, pl, vh, wave * 4 + q4, r, rows, start, pos, qs, kvs);
+      if constexpr (STAMP) ts[2] = phase_clock();
+      if (pro) {
+        PrologueLoads pl;
+        pl.wv = pp.wv;
+        pl.cv = pp.cv;
+        pl.sv = pp.sv;
+        pl.xv = partials_sum(a, pp);
+        prologue_finish(a, pl, vh, plg, r, rows, start, pos, qs, kvs);
+      }
     } else {
       if (n > 0) {
 #pragma unroll
         for (int d = 0; d + 1 < NS; ++d) issue(d, d);
       }
-      owns_slot = fused_prologue(a, vh, wave * 4 + q4, r, rows, start, pos, qs, kvs);
+      if (pro) fused_prologue(a, vh, plg, r, rows, start, pos, qs, kvs);
     }
     __syncthreads();
+    if constexpr (STAMP) ts[3] = phase_clock();
 #pragma unroll
     for (int s = 0; s < 4; ++s) qa[s] = r < rows ? qs[r][q4 + 4 * s] : make_uint4(0, 0, 0, 0);
     subst = owns_slot && pos < end;
@@ -652,6 +698,7 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
       for (int d = 0; d + 1 < NS; ++d) issue(d, d);
     }
+    if constexpr (STAMP) ts[2] = ts[3] = phase_clock();
   }
 
   // This lane's query r: running maximum and partial denominator over the
@@ -734,16 +781,28 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
         if (!done) {
           issue((d + NS - 1) % NS, i + d + NS - 1);
           consume(d, i + d);
+          if constexpr (STAMP) {
+            if (i + d == 0) ts[4] = phase_clock();
+          }
           done = i + d + 1 >= n;
         }
       }
       if (done) break;
     }
   }
+  if constexpr (STAMP) {
+    if (n == 0) ts[4] = phase_clock();
+    ts[5] = phase_clock();
+  }
 
   // Wave totals through LDS: query g's maximum and denominator (summed over
-  // its four key lanes) from lane g, O rows from lanes 0..15; wave 0's lanes
-  // 0..15 then take query g's dims 8r..8r+8 of every wave, in wave order.
+  // its four key lanes) from lane g, O rows from lanes 0..15.  Then every
+  // thread merges at once: wave g takes query row g (g < rows), lane l its
+  // dims 2l and 2l + 1, each wave's share weighted by 2^(m_w - M) against
+  // the row's overall maximum M.  (Wave 0 merging the waves one after
+  // another - rescaling its running state per wave, four rows of 8 dims per
+  // lane - took 1.7 us per workgroup, measured with the phase stamps; this
+  // takes a few hundred nanoseconds.)
   float lt = lq + __shfl_xor(lq, 16);
   lt += __shfl_xor(lt, 32);
   if (lane < GT) {
@@ -757,69 +816,100 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
       for (int g = 0; g < GT; ++g) xacc[wave][g][16 * db + r] = oacc[db][g];
   }
   __syncthreads();
-  State<GT> st;
-  if (wave == 0 && lane < 16) {
+  if constexpr (STAMP) ts[12] = phase_clock();
+  const int gq = wave;  // this wave's query row
+  const bool owner = gq < rows;
+  float rm = kNegInf, rl = 0.0f, r0 = 0.0f, r1 = 0.0f;
+  if (owner) {
+    float mw[kW], lw[kW];
+    float2 ow[kW];
 #pragma unroll
-    for (int g = 0; g < GT; ++g) {
-      st.m[g] = xm[0][g];
-      st.l[g] = xl[0][g];
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) st.acc[g][jj] = xacc[0][g][8 * r + jj];
+    for (int w = 0; w < kW; ++w) {
+      mw[w] = xm[w][gq];
+      lw[w] = xl[w][gq];
+      ow[w] = *reinterpret_cast<const float2*>(&xacc[w][gq][2 * lane]);
     }
 #pragma unroll
-    for (int w = 1; w < kW; ++w)
+    for (int w = 0; w < kW; ++w) rm = fmaxf(rm, mw[w]);
+    const float base = rm == kNegInf ? 0.0f : rm;  // no valid key: every weight 0
 #pragma unroll
-      for (int g = 0; g < GT; ++g) {
-        float o8[8];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) o8[jj] = xacc[w][g][8 * r + jj];
-        merge_row<GT>(st, g, xm[w][g], xl[w][g], o8);
-      }
+    for (int w = 0; w < kW; ++w) {
+      const float c = exp2_hw(mw[w] - base);
+      rl = __builtin_fmaf(lw[w], c, rl);
+      r0 = __builtin_fmaf(ow[w].x, c, r0);
+      r1 = __builtin_fmaf(ow[w].y, c, r1);
+    }
   }
-  const bool owner = wave == 0 && lane < 16;
-  if (a.splits == 1) {
-    if (!owner) return;
-#pragma unroll
-    for (int g = 0; g < GT; ++g) {
-      if (g >= rows) break;
-      const float den = st.l[g] > 0.0f ? st.l[g] : 1.0f;
-      float o[8];
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) o[jj] = st.acc[g][jj] / den;
-      store16<false>(a.out + ((int64_t)vh * G + g) * kD + 8 * r, pack8(o));
+  // Instrumented build: every wave stores its own stamps (lane 0, ordinary
+  // vector stores); thread 0 waits for the output stores, takes the last
+  // stamp and stores wave 0's.
+  uint64_t* const stamp_row = STAMP ? a.stamps + ((int64_t)seg * gridDim.x + vh) * kPhases : nullptr;
+  if constexpr (STAMP) {
+    ts[6] = phase_clock();
+    if (lane == 0) {
+      stamp_row[8 + wave] = ts[5];
+      if (wave > 0) stamp_row[12 + wave] = ts[4];
     }
+  }
+  auto record = [&]() {
+    if constexpr (STAMP) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      ts[7] = phase_clock();
+      if (threadIdx.x == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) stamp_row[i] = ts[i];
+        stamp_row[12] = ts[12];
+      }
+    }
+  };
+  if (a.splits == 1) {
+    if (!owner) return;  // wave 0 always owns row 0
+    const float den = rl > 0.0f ? rl : 1.0f;
+    reinterpret_cast<uint32_t*>(a.out + ((int64_t)vh * G + gq) * kD)[lane] = pack2(r0 / den, r1 / den);
+    record();
     return;
   }
   if (owner) {
     const int64_t slot = (int64_t)vh * a.splits + seg;
-#pragma unroll
-    for (int g = 0; g < GT; ++g) {
-      if (g >= rows) break;
-      float* dst = a.partials + (slot * G + g) * kD + 8 * r;
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) dst[jj] = st.acc[g][jj];
-      if (r == 0) {
-        a.stats[slot * 2 * G + g] = st.m[g];
-        a.stats[slot * 2 * G + G + g] = st.l[g];
-      }
+    *reinterpret_cast<float2*>(a.partials + (slot * G + gq) * kD + 2 * lane) = make_float2(r0, r1);
+    if (lane == 0) {
+      a.stats[slot * 2 * G + gq] = rm;
+      a.stats[slot * 2 * G + G + gq] = rl;
     }
   }
+  record();
 }
 
 // One wave per query row, four rows per workgroup.
 constexpr int kMergeRows = kBlock / kWave;
+template <bool STAMP = false>
 __global__ __launch_bounds__(kBlock) void attn_merge_kernel(AttnArgs a, int64_t rows) {
+  uint64_t ts[kMergePhases] = {};
+  if constexpr (STAMP) ts[0] = phase_clock();
   const int64_t row = (int64_t)blockIdx.x * kMergeRows + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
   const int G = a.groups;
   const int64_t vh = row / G;
   const int g = (int)(row - vh * G);
-  reinterpret_cast<uint32_t*>(a.out + row * kD)[lane] =
-      merge_segments_row(a.partials, a.stats, vh, a.splits, G, g, lane);
+  const uint32_t merged = merge_segments_row(a.partials, a.stats, vh, a.splits, G, g, lane);
+  if constexpr (STAMP) {
+    asm volatile("" ::"v"(merged));
+    ts[1] = phase_clock();
+  }
+  reinterpret_cast<uint32_t*>(a.out + row * kD)[lane] = merged;
+  if constexpr (STAMP) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    ts[2] = phase_clock();
+    if (threadIdx.x == 0) {
+      uint64_t* dst = a.stamps + kMergePhases * (int64_t)blockIdx.x;
+#pragma unroll
+      for (int i = 0; i < kMergePhases; ++i) dst[i] = ts[i];
+    }
+  }
 }
 
-template <int GT, bool FUSED>
+template <int GT, bool FUSED, bool STAMP = false>
 int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
   // Two sets of U = 2 key blocks in flight per wave.  Measured on the engine's
   // workloads (batch x keys = 1 x 545, 4 x 2081, 16 x 641, 64 x 1024): U = 4
@@ -834,10 +924,21 @@ int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
     // K/V stream once per step: nontemporal loads (measured 2-15% faster from
     // batch 1 x 545 to 64 x 1024 keys; the bandwidth of a plain read of this
     // access pattern rises from 5.6 to 6.1-6.7 TB/s).
-    hipLaunchKernelGGL((attn_mfma_kernel<GT, FUSED, true>), dim3((unsigned)vheads, (unsigned)a.splits),
-                       dim3(kBlock), 0, s, a);
+    const dim3 grid((unsigned)vheads, (unsigned)a.splits);
+    if constexpr (!FUSED) {
+      static_assert(!STAMP, "the instrumented build times the fused entry point");
+      hipLaunchKernelGGL((attn_mfma_kernel<GT, kProNone, true>), grid, dim3(kBlock), 0, s, a);
+    } else if (a.qkv_splits == 0) {
+      hipLaunchKernelGGL((attn_mfma_kernel<GT, kProRows, true, 2, STAMP>), grid, dim3(kBlock), 0, s, a);
+    } else if (a.qkv_splits <= kPrologueSplits) {
+      hipLaunchKernelGGL((attn_mfma_kernel<GT, kProPartials, true, 2, STAMP>), grid, dim3(kBlock), 0, s,
+                         a);
+    } else {
+      hipLaunchKernelGGL((attn_mfma_kernel<GT, kProMany, true, 2, STAMP>), grid, dim3(kBlock), 0, s, a);
+    }
     st = launch_status();
   } else {
+    static_assert(!STAMP, "the instrumented build times the matrix-core kernel");
     for (a.g0 = 0; a.g0 < a.groups && st == QF_OK; a.g0 += GT) {
       hipLaunchKernelGGL((attn_kernel<GT, U, 4, FUSED>), dim3((unsigned)vheads, (unsigned)a.splits),
                          dim3(kBlock), 0, s, a);
@@ -846,8 +947,9 @@ int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
   }
   if (st != QF_OK || a.splits == 1 || !a.out) return st;  // no out: segments stay unmerged
   const int64_t rows = vheads * a.groups;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)((rows + kMergeRows - 1) / kMergeRows)), dim3(kBlock), 0,
-                     s, a, rows);
+  if constexpr (STAMP) a.stamps += (int64_t)vheads * a.splits * kPhases;  // after the attention's
+  hipLaunchKernelGGL(attn_merge_kernel<STAMP>, dim3((unsigned)((rows + kMergeRows - 1) / kMergeRows)),
+                     dim3(kBlock), 0, s, a, rows);
   return launch_status();
 }
 
@@ -922,6 +1024,30 @@ int dispatch_attn(const AttnArgs& a, int64_t vheads, hipStream_t s) {
   }
 }
 
+// Fills the attention half of `a` for the fused entry points.
+int fused_setup(AttnArgs& a, const void* qkv, int32_t qkv_splits, const void* q_weight,
+                const void* k_weight, float q_eps, float k_eps, const void* cos, const void* sin,
+                const int64_t* position, void* key_cache, void* value_cache, int64_t batch,
+                int32_t q_heads, int32_t kv_heads) {
+  if (qkv_splits < 0 || !q_weight || !k_weight || !cos || !sin || !position) return QF_E_ARG;
+  if (!aligned16(q_weight) || !aligned16(k_weight) || !aligned16(cos) || !aligned16(sin) ||
+      (reinterpret_cast<uintptr_t>(position) & 7u))
+    return QF_E_ALIGN;
+  a.qkv = qkv;
+  a.qkv_splits = qkv_splits;
+  a.qkv_stride = batch * ((int64_t)q_heads + 2 * (int64_t)kv_heads) * kD;
+  a.qw = static_cast<const uint16_t*>(q_weight);
+  a.kw = static_cast<const uint16_t*>(k_weight);
+  a.q_eps = q_eps;
+  a.k_eps = k_eps;
+  a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin);
+  a.position = position;
+  a.kc = static_cast<uint16_t*>(key_cache);
+  a.vc = static_cast<uint16_t*>(value_cache);
+  return QF_OK;
+}
+
 }  // namespace
 
 extern "C" int qf_decode_attention(const void* q, const void* k, const void* v,
@@ -950,21 +1076,41 @@ extern "C" int qf_decode_attention_qkv(const void* qkv, int32_t qkv_splits, cons
   const int st = attention_setup(qkv, key_cache, value_cache, used, batch, q_heads, kv_heads,
                                  capacity, scale, splits, span, partials, stats, out, a, vheads);
   if (st != QF_OK) return st;
-  if (qkv_splits < 0 || !q_weight || !k_weight || !cos || !sin || !position) return QF_E_ARG;
-  if (!aligned16(q_weight) || !aligned16(k_weight) || !aligned16(cos) || !aligned16(sin) ||
-      (reinterpret_cast<uintptr_t>(position) & 7u))
-    return QF_E_ALIGN;
-  a.qkv = qkv;
-  a.qkv_splits = qkv_splits;
-  a.qkv_stride = batch * ((int64_t)q_heads + 2 * (int64_t)kv_heads) * kD;
-  a.qw = static_cast<const uint16_t*>(q_weight);
-  a.kw = static_cast<const uint16_t*>(k_weight);
-  a.q_eps = q_eps;
-  a.k_eps = k_eps;
-  a.cos = static_cast<const uint16_t*>(cos);
-  a.sin = static_cast<const uint16_t*>(sin);
-  a.position = position;
-  a.kc = static_cast<uint16_t*>(key_cache);
-  a.vc = static_cast<uint16_t*>(value_cache);
+  const int fs = fused_setup(a, qkv, qkv_splits, q_weight, k_weight, q_eps, k_eps, cos, sin,
+                            position, key_cache, value_cache, batch, q_heads, kv_heads);
+  if (fs != QF_OK) return fs;
   return dispatch_attn<true>(a, vheads, as_stream(stream));
 }
+
+#ifdef QF_PHASE_STAMPS
+// Instrumented qf_decode_attention_qkv for phase timing (built only into the
+// measurement library, never into libqwen_fused.so): same arguments and
+// results, query groups of at most 4 rows (the matrix-core kernel), plus
+// `stamps`, u64 [virtual heads * splits * kPhases] for the attention's
+// workgroups (index (split * virtual heads + vh) * kPhases + phase) followed,
+// when splits > 1, by [merge workgroups * kMergePhases] for the merge.
+extern "C" int qf_decode_attention_qkv_phases(
+    const void* qkv, int32_t qkv_splits, const void* q_weight, const void* k_weight, float q_eps,
+    float k_eps, const void* cos, const void* sin, const int64_t* position, void* key_cache,
+    void* value_cache, const int32_t* used, int64_t batch, int32_t q_heads, int32_t kv_heads,
+    int64_t capacity, float scale, int32_t splits, int64_t span, float* partials, float* stats,
+    void* out, uint64_t* stamps, void* stream) {
+  AttnArgs a;
+  int64_t vheads = 0;
+  const int st = attention_setup(qkv, key_cache, value_cache, used, batch, q_heads, kv_heads,
+                                 capacity, scale, splits, span, partials, stats, out, a, vheads);
+  if (st != QF_OK) return st;
+  if (!stamps) return QF_E_ARG;
+  if (a.groups > 4) return QF_E_SHAPE;
+  const int fs = fused_setup(a, qkv, qkv_splits, q_weight, k_weight, q_eps, k_eps, cos, sin,
+                            position, key_cache, value_cache, batch, q_heads, kv_heads);
+  if (fs != QF_OK) return fs;
+  a.stamps = stamps;
+  hipStream_t s = as_stream(stream);
+  switch (a.groups) {
+    case 1: return launch_attn<1, true, true>(a, vheads, s);
+    case 2: return launch_attn<2, true, true>(a, vheads, s);
+    default: return launch_attn<4, true, true>(a, vheads, s);
+  }
+}
+#endif
