@@ -22,7 +22,8 @@ is per workgroup), in microseconds:
   first key loads issued -> queries ready (barrier) -> first key block
   consumed -> key loop done -> waves merged -> stored and acknowledged;
 * the gap from the last attention workgroup's end to the first merge
-  workgroup's start (the launch hand-off), and the merge's own phases;
+  workgroup's start (the launch hand-off), and the merge's own phases
+  (entry -> its loads landed -> merged -> stored and acknowledged);
 * the gap from one call's merge end to the next call's first start.
 
 Run: ``python -m starter_amd.attention_phases`` (needs an MI355X and the
@@ -153,6 +154,7 @@ def measure(batch: int, keys: int, qkv_splits: int, calls: int = 24, replays: in
 
     stamped = graph_of(True)
     rows = {name: [] for name in ("span", "spread", "handoff", "next_call", "merge_load",
+                                  "merge_combine",
                                   "merge_store", "attention_span", "first_block_spread",
                                   *PHASE_NAMES, *BARRIER_NAMES)}
     for _ in range(replays):
@@ -181,7 +183,8 @@ def measure(batch: int, keys: int, qkv_splits: int, calls: int = 24, replays: in
             if merge_blocks:
                 mer = row[vheads * splits * PHASES:].view(merge_blocks, MERGE_PHASES).double()
                 rows["handoff"].append((float(mer[:, 0].min()) - att_end) / clock)
-                rows["merge_load"].extend(((mer[:, 1] - mer[:, 0]) / clock).tolist())
+                rows["merge_load"].extend(((mer[:, 3] - mer[:, 0]) / clock).tolist())
+                rows["merge_combine"].extend(((mer[:, 1] - mer[:, 3]) / clock).tolist())
                 rows["merge_store"].extend(((mer[:, 2] - mer[:, 1]) / clock).tolist())
                 end = float(mer[:, 2].max())
             rows["span"].append((end - first) / clock)
@@ -226,7 +229,8 @@ def table(results) -> str:
     line("  of phase 6: wave 0's merge of the four waves", BARRIER_NAMES[2])
     line("spread of the four waves' first-block times", "first_block_spread")
     line("hand-off: last attention store → first merge start", "handoff")
-    line("merge: start → merged (loads landed)", "merge_load")
+    line("merge: start → its loads landed", "merge_load")
+    line("merge: loads landed → merged", "merge_combine")
     line("merge: merged → stored", "merge_store")
     line("next call: last store → next call's first start", "next_call")
     return "\n".join(lines)

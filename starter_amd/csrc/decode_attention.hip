@@ -87,7 +87,8 @@ struct AttnArgs {
 //   7 the output or partials are stored and acknowledged; 12 every wave has
 //   passed the barrier before the merge.
 // Wave w: 8 + w its key loop done; 12 + w (w > 0) its first block consumed.
-// The merge kernel records 0 entry, 1 merged, 2 stored and acknowledged.
+// The merge kernel records 0 entry, 3 its first loads landed, 1 merged,
+// 2 stored and acknowledged.
 constexpr int kPhases = 16;
 constexpr int kMergePhases = 4;
 
@@ -882,7 +883,7 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a) {
 
 // One wave per query row, four rows per workgroup.
 constexpr int kMergeRows = kBlock / kWave;
-template <bool STAMP = false>
+template <int NB, bool STAMP = false>
 __global__ __launch_bounds__(kBlock) void attn_merge_kernel(AttnArgs a, int64_t rows) {
   uint64_t ts[kMergePhases] = {};
   if constexpr (STAMP) ts[0] = phase_clock();
@@ -892,7 +893,13 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(AttnArgs a, int64_t 
   const int G = a.groups;
   const int64_t vh = row / G;
   const int g = (int)(row - vh * G);
-  const uint32_t merged = merge_segments_row(a.partials, a.stats, vh, a.splits, G, g, lane);
+  SegmentLoads<NB> L;
+  merge_issue(L, a.partials, a.stats, vh, a.splits, G, g, lane);
+  if constexpr (STAMP) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    ts[3] = phase_clock();
+  }
+  const uint32_t merged = merge_finish(L, a.partials, vh, a.splits, G, g, lane);
   if constexpr (STAMP) {
     asm volatile("" ::"v"(merged));
     ts[1] = phase_clock();
@@ -948,8 +955,19 @@ int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
   if (st != QF_OK || a.splits == 1 || !a.out) return st;  // no out: segments stay unmerged
   const int64_t rows = vheads * a.groups;
   if constexpr (STAMP) a.stamps += (int64_t)vheads * a.splits * kPhases;  // after the attention's
-  hipLaunchKernelGGL(attn_merge_kernel<STAMP>, dim3((unsigned)((rows + kMergeRows - 1) / kMergeRows)),
-                     dim3(kBlock), 0, s, a, rows);
+  // Segment loads per batch: the fewest of 2, 4, 8, 12, 16 that cover the
+  // split count (one batch up to 16 segments, two for 17-32).
+  const dim3 grid((unsigned)((rows + kMergeRows - 1) / kMergeRows));
+  if (a.splits <= 2)
+    hipLaunchKernelGGL((attn_merge_kernel<2, STAMP>), grid, dim3(kBlock), 0, s, a, rows);
+  else if (a.splits <= 4)
+    hipLaunchKernelGGL((attn_merge_kernel<4, STAMP>), grid, dim3(kBlock), 0, s, a, rows);
+  else if (a.splits <= 8)
+    hipLaunchKernelGGL((attn_merge_kernel<8, STAMP>), grid, dim3(kBlock), 0, s, a, rows);
+  else if (a.splits <= 12)
+    hipLaunchKernelGGL((attn_merge_kernel<12, STAMP>), grid, dim3(kBlock), 0, s, a, rows);
+  else
+    hipLaunchKernelGGL((attn_merge_kernel<16, STAMP>), grid, dim3(kBlock), 0, s, a, rows);
   return launch_status();
 }
 

@@ -34,43 +34,56 @@ __device__ __forceinline__ float lane_value(float v, int lane) {
 // first batch's loads (merge_issue) and their use (merge_finish): vector
 // loads complete in order, so loads issued after the first batch do not
 // delay its combine.  Must be called by all 64 lanes of a wave.
+template <int NB = kMergeBatch>
 struct SegmentLoads {
-  float2 p[kMergeBatch];
+  float2 p[NB];
   float m, l;  // lane s: segment s's running maximum and denominator
 };
 
-__device__ __forceinline__ void merge_load_batch(SegmentLoads& L, const float* partials,
+template <int NB>
+__device__ __forceinline__ void merge_load_batch(SegmentLoads<NB>& L, const float* partials,
                                                  int64_t vh, int S, int G, int g, int lane, int s0) {
   const float* base = partials + (vh * S * G + g) * 128 + 2 * lane;
   const int seg_stride = G * 128;
 #pragma unroll
-  for (int i = 0; i < kMergeBatch; ++i) {
+  for (int i = 0; i < NB; ++i) {
     const int s = s0 + i < S ? s0 + i : S - 1;
     L.p[i] = *reinterpret_cast<const float2*>(base + s * seg_stride);
   }
 }
 
-__device__ __forceinline__ void merge_issue(SegmentLoads& L, const float* partials, const float* stats,
-                                            int64_t vh, int S, int G, int g, int lane) {
+template <int NB>
+__device__ __forceinline__ void merge_issue(SegmentLoads<NB>& L, const float* partials,
+                                            const float* stats, int64_t vh, int S, int G, int g,
+                                            int lane) {
   merge_load_batch(L, partials, vh, S, G, g, lane, 0);
   const float* st = stats + vh * S * 2 * G + g;
   L.m = lane < S ? st[lane * 2 * G] : -__builtin_inff();
   L.l = lane < S ? st[lane * 2 * G + G] : 0.0f;
 }
 
-__device__ __forceinline__ uint32_t merge_finish(SegmentLoads& L, const float* partials, int64_t vh,
-                                                 int S, int G, int g, int lane) {
-  static_assert(kMaxSegments == 2 * kMergeBatch, "at most two batches");
-  float M = -__builtin_inff();
-#pragma unroll
-  for (int s = 0; s < kMaxSegments; ++s) M = fmaxf(M, lane_value(L.m, s));
+// NB segments per batch (up to kMergeBatch): a caller that knows S <= NB
+// issues no loads for slots it does not need; the sums are the same for
+// every NB (each term added in segment order).
+template <int NB>
+__device__ __forceinline__ uint32_t merge_finish(SegmentLoads<NB>& L, const float* partials,
+                                                 int64_t vh, int S, int G, int g, int lane) {
+  static_assert(NB >= 1 && NB <= kMergeBatch && kMaxSegments == 32, "batch within a wave");
+  // M = max over lanes 0..31 (lane s >= S holds -inf): a max within each
+  // 16-lane row by DPP, then rows 0 and 1 (a max is exact in any order).
+  float rm = L.m;
+  rm = fmaxf(rm, __uint_as_float(dpp_u32<kQuadXor1>(__float_as_uint(rm))));
+  rm = fmaxf(rm, __uint_as_float(dpp_u32<kQuadXor2>(__float_as_uint(rm))));
+  rm = fmaxf(rm, __uint_as_float(dpp_u32<kRowHalfMirror>(__float_as_uint(rm))));
+  rm = fmaxf(rm, __uint_as_float(dpp_u32<kRowMirror>(__float_as_uint(rm))));
+  float M = fmaxf(lane_value(rm, 0), lane_value(rm, 16));
   if (M == -__builtin_inff()) M = 0.0f;
   const float w_own = L.l > 0.0f ? __builtin_amdgcn_exp2f(L.m - M) : 0.0f;
   const float lw_own = L.l * w_own;
   float total = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
   auto combine = [&](int s0) {
 #pragma unroll
-    for (int i = 0; i < kMergeBatch; ++i) {
+    for (int i = 0; i < NB; ++i) {
       const bool on = s0 + i < S;
       const float w = lane_value(w_own, s0 + i);
       const float lw = lane_value(lw_own, s0 + i);
@@ -80,17 +93,18 @@ __device__ __forceinline__ uint32_t merge_finish(SegmentLoads& L, const float* p
     }
   };
   combine(0);
-  if (S > kMergeBatch) {
-    merge_load_batch(L, partials, vh, S, G, g, lane, kMergeBatch);
-    combine(kMergeBatch);
+  for (int s0 = NB; s0 < S; s0 += NB) {
+    merge_load_batch(L, partials, vh, S, G, g, lane, s0);
+    combine(s0);
   }
   const float den = total > 0.0f ? total : 1.0f;
   return pack2(acc0 / den, acc1 / den);
 }
 
+template <int NB = kMergeBatch>
 __device__ __forceinline__ uint32_t merge_segments_row(const float* partials, const float* stats,
                                                        int64_t vh, int S, int G, int g, int lane) {
-  SegmentLoads L;
+  SegmentLoads<NB> L;
   merge_issue(L, partials, stats, vh, S, G, g, lane);
   return merge_finish(L, partials, vh, S, G, g, lane);
 }

@@ -438,7 +438,7 @@ __global__ __launch_bounds__(kBlock) void skinny_kernel(SkinnyArgs a) {
   // workgroup takes part.
   const int heads = XM ? a.chunks * kChunk / 128 : 0;  // heads in this split's K range
   const int q0 = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform by construction
-  SegmentLoads seg;
+  SegmentLoads<> seg;
   auto pair = [&](int q, int64_t& vh, int& g, int& off) {
     const int m = q / heads, hl = q - m * heads, h = (int)(kbase / 128) + hl;
     vh = (int64_t)m * a.seg_kv_heads + h / a.seg_groups;

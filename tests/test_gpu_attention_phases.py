@@ -57,6 +57,6 @@ def test_stamped_attention_equals_product(batch, keys, qkv_splits):
     att = stamps[:vheads * plan.splits * ph.PHASES].view(-1, ph.PHASES)[:, :8].cpu()
     assert bool((att > 0).all()) and bool((att[:, 1:] >= att[:, :-1]).all())
     if merge_blocks:
-        mer = stamps[vheads * plan.splits * ph.PHASES:].view(-1, ph.MERGE_PHASES)[:, :3].cpu()
+        mer = stamps[vheads * plan.splits * ph.PHASES:].view(-1, ph.MERGE_PHASES)[:, [0, 3, 1, 2]].cpu()
         assert bool((mer > 0).all()) and bool((mer[:, 1:] >= mer[:, :-1]).all())
         assert int(mer[:, 0].min()) >= int(att[:, 0].min())
