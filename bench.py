@@ -686,12 +686,26 @@ def torch_cpu_configs(reps_small: int = 20, reps_large: int = 3) -> dict:
         record("config4a_add_rms_norm_8192x2560", timed(add_norm, reps_large), TOKENS,
                BYTES["add_rms_norm"])
 
-        q4, k4 = draw((B, T, NQ, D)), draw((B, T, NK, D))
+        # Config 4b as the GPU leg runs it (prefill_qkv at the engine's call
+        # site, engine/prefill.py:39-43): the packed Q|K|V rows' per-head
+        # norm + RoPE, K written into the cache, V copied into it.
         cos4, sin4 = tables(torch.arange(T))
         cos4, sin4 = cos4.view(1, 1, T, D), sin4.view(1, 1, T, D)
-        record("config4b_qk_norm_rope_4x2048", timed(lambda: qk_rope(q4, k4, cos4, sin4), reps_large),
-               TOKENS * (NQ + NK), bf16_bytes(2 * TOKENS * (NQ + NK) * D, 2 * D, 2 * T * D))
-        del res4, hid4, q4, k4
+        qkv4 = draw((TOKENS, (NQ + 2 * NK) * D))
+        keys4 = torch.zeros((B, NK, CAPACITY, D), dtype=BF16)
+        values4 = torch.zeros_like(keys4)
+
+        def packed_qkv():
+            heads = qkv4.view(B, T, NQ + 2 * NK, D).transpose(1, 2)      # [B, H, T, D]
+            qn, kn = norm(heads[:, :NQ], qw), norm(heads[:, NQ:NQ + NK], kw)
+            q = qn * cos4 + rotate_half(qn) * sin4
+            keys4[:, :, :T] = kn * cos4 + rotate_half(kn) * sin4
+            values4[:, :, :T] = heads[:, NQ + NK:]
+            return q
+
+        record("config4b_prefill_qkv_4x2048", timed(packed_qkv, reps_large), TOKENS * (NQ + 2 * NK),
+               BYTES["prefill_qkv"])
+        del res4, hid4, qkv4, keys4, values4
 
         gate_up = draw((TOKENS, 2 * I))
         record("config5a_silu_mul_8192x9728",
@@ -917,6 +931,7 @@ def main() -> int:
                       decode.get("config2_add_rms_norm_64x2560_x36", {}).get("us_per_call"),
                   "config3_qk_norm_rope_b32": decode.get("config3_qk_norm_rope_b32", {}).get("us_per_call"),
                   "config4a_add_rms_norm_8192x2560": kernels["add_rms_norm"]["us_per_call_mean"],
+                  "config4b_prefill_qkv_4x2048": kernels["prefill_qkv"]["us_per_call_mean"],
                   "config5a_silu_mul_8192x9728": kernels["silu_mul"]["us_per_call_mean"],
                   "config5b_embedding_8192_ids": kernels["embedding"]["us_per_call_mean"]}
         for name, entry in result["cpu_reference"]["configs"].items():
