@@ -16,11 +16,20 @@
 // i.e. G QB / 16 tiles of 16 query rows (one head, 16 positions); wave w
 // takes tiles w, w + W, ...  Workgroups run longest first (the last query
 // blocks attend the most keys).  Keys stream in blocks of 64, staged once per
-// workgroup in LDS (cooperative 16-byte loads into one of two buffers, the
-// next block's loads in flight during this block's arithmetic) and shared by
-// every tile, so the K/V bytes a CU pulls from L2 per flop shrink with the
-// workgroup's query rows (the per-CU L2 request rate, not the matrix cores,
-// bounded the 4-wave form).
+// workgroup in LDS and shared by every tile, so the K/V bytes a CU pulls from
+// L2 per flop shrink with the workgroup's query rows (the per-CU L2 request
+// rate, not the matrix cores, bounded the 4-wave form).  The blocks go from
+// the cache straight into LDS (global_load_lds_dwordx4), K one block ahead
+// of V, so no registers hold them in flight.
+//
+// Pipeline (per wave): block j + 1's score products run on the matrix cores
+// while the VALU does block j's softmax (one scheduling region, interleaved
+// one product to five VALU instructions), then block j's P V.  The softmax
+// VALU work (an exp2, an FMA, a sum, a maximum and half a conversion per
+// score) costs about as many SIMD cycles as the products, so the two only
+// reach the matrix-core bound together; measured (counters, 4 x 2048): the
+// matrix cores 32% busy and the VALU 41% before, with little of the two
+// overlapping.
 //
 // Both products are on the matrix cores (v_mfma_f32_16x16x32_bf16):
 // * Scores, transposed: S^T = K Q^T for a 16-key tile is a chain of four
@@ -38,7 +47,7 @@
 // Each lane keeps the running maximum and denominator of its own query
 // (l % 16) over its own keys; the accumulators of query row r are rescaled
 // with the factor of the lanes that own query r (fetched by shuffles) when
-// some maximum of the tile moved.  K rows in LDS are 272 bytes (the score
+// some row maximum grew past its reference by more than kLazy.  K rows in LDS are 272 bytes (the score
 // reads, 16 keys at one column per 16-lane group, fall on distinct banks),
 // V rows 288 bytes (the transposing reads, 4 keys x 4 column groups per
 // 16-lane group, on distinct banks).  Keys at or past `length` are never
@@ -114,36 +123,32 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
   constexpr int QB = Split<G, WIDE>::QB;
   constexpr int TPW = Split<G, WIDE>::TPW;
   constexpr int W = Split<G, WIDE>::W;
-  constexpr int kThreads = W * kWave;
   constexpr int kSubs = QB / 16;  // position tiles per head
-  constexpr int kLoadsPerThread = kKB * kD * 2 / 16 / kThreads;  // 16-byte loads per operand
+  constexpr int kKLoads = kKB * kKRow / 1024;  // 1 KB direct loads per staged K block (17)
+  constexpr int kVLoads = kKB * kVRow / 1024;  // ... per V block (18)
+  constexpr int kKPerWave = (kKLoads + W - 1) / W;
+  constexpr int kVPerWave = (kVLoads + W - 1) / W;
   static_assert(G * kSubs == W * TPW, "every wave holds TPW tiles");
   static_assert(W % kSubs == 0, "a wave's tiles share their positions");
   static_assert(W * 16 * kORow <= 2 * kKB * kKRow, "output staging fits the K buffers");
-  // Two K/V block buffers: block j + 1 is staged into one while block j is
-  // read from the other, so one barrier per block separates the two.
-  __shared__ __attribute__((aligned(16))) uint8_t klds[2][kKB * kKRow];
-  __shared__ __attribute__((aligned(16))) uint8_t vlds[2][kKB * kVRow];
+  static_assert(kKB * kKRow % 1024 == 0 && kKB * kVRow % 1024 == 0, "whole 1 KB loads");
+  __shared__ __attribute__((aligned(1024))) uint8_t klds[2][kKB * kKRow];
+  __shared__ __attribute__((aligned(1024))) uint8_t vlds[2][kKB * kVRow];
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int r = lane % 16;
   const int g4 = lane / 16;
-  // Longest workgroups first: the block index runs over (query block
-  // descending, then sequence x KV head).
   const int qb = a.qblocks - 1 - (int)(blockIdx.x / a.pairs);
   const int pair = (int)(blockIdx.x % a.pairs);
   const int b = pair / a.kv_heads;
   const int kvh = pair % a.kv_heads;
   const int64_t p0 = (int64_t)qb * QB;
   const int64_t last = a.length - 1;
-  const int nkb = (int)(p0 / kKB) + 1;  // key blocks: all below the diagonal one, and it
+  const int nkb = (int)(p0 / kKB) + 1;
   const uint16_t* kbase = a.k + (int64_t)pair * a.capacity * kD;
   const uint16_t* vbase = a.v + (int64_t)pair * a.capacity * kD;
 
-  // This wave's tiles: tile tau = wave + W u -> head kvh G + tau / kSubs,
-  // positions p0 + 16 (tau % kSubs) .. +16 (the same positions for every
-  // tile of a wave, since kSubs divides W).
   const int64_t pt = p0 + 16 * (wave % kSubs);
   int head[TPW];
   uint4 qf[TPW][4];
@@ -169,38 +174,69 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
     for (int db = 0; db < 8; ++db) o[u][db] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Cooperative block loads: thread tid moves 16-byte chunk tid % 16 of keys
-  // tid / 16 + (kThreads / 16) i of the block, for K and for V.
-  uint4 kreg[kLoadsPerThread], vreg[kLoadsPerThread];
-  const int chunk = tid % 16;
-  auto fetch = [&](int j) {
+  // Blocks move from the cache straight into LDS (global_load_lds_dwordx4:
+  // lane l of a load writes 16 bytes at the load's 1 KB segment + 16 l), so no
+  // registers hold them in flight.  Staged rows keep their padding (K 272,
+  // V 288 bytes): linear 16-byte slot L of a buffer is slot L % (row / 16) of
+  // row L / (row / 16); lanes on a padding slot re-read the row's first chunk
+  // (the bytes land in the padding, never read).  Load i of a block is
+  // issued by wave i % W.  Per lane the (row, chunk) of each of its loads is
+  // fixed, so its byte offset inside a block is computed once.
+  int koff[kKPerWave], voff[kVPerWave];
 #pragma unroll
-    for (int i = 0; i < kLoadsPerThread; ++i) {
-      int64_t key = (int64_t)j * kKB + tid / 16 + (kThreads / 16) * i;
-      key = key < a.length ? key : last;
-      kreg[i] = load16<true>(kbase + key * kD + 8 * chunk);
-      vreg[i] = load16<true>(vbase + key * kD + 8 * chunk);
+  for (int i = 0; i < kKPerWave; ++i) {
+    const int L = 64 * (wave + W * i) + lane;
+    const int row = L / (kKRow / 16), slot = L % (kKRow / 16);
+    koff[i] = row * (kD * 2) + (slot < 16 ? 16 * slot : 0);
+  }
+#pragma unroll
+  for (int i = 0; i < kVPerWave; ++i) {
+    const int L = 64 * (wave + W * i) + lane;
+    const int row = L / (kVRow / 16), slot = L % (kVRow / 16);
+    voff[i] = row * (kD * 2) + (slot < 16 ? 16 * slot : 0);
+  }
+  // Rows at or past `length` (the last block only) re-read row length - 1.
+  auto load_block = [&](const uint16_t* base, uint8_t* dst, const int* off, int count, int loads,
+                        int j, bool clamp) {
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(base) + (int64_t)j * kKB * kD * 2;
+#pragma unroll
+    for (int i = 0; i < count; ++i) {
+      const int li = wave + W * i;
+      if (li < loads) {  // wave-uniform
+        int o_ = off[i];
+        if (clamp) {
+          const int64_t row = (int64_t)j * kKB + o_ / (kD * 2);
+          if (row > last) o_ = (int)(last - (int64_t)j * kKB) * (kD * 2) + o_ % (kD * 2);
+        }
+        // Issued as inline assembly: the compiler's wait counting would
+        // otherwise order every later LDS read after these loads, though
+        // they fill a buffer no read of this block touches.  The block's
+        // loads are waited for explicitly (vmcnt(0)) before its barrier.
+        const uint32_t m0 = (uint32_t)(uintptr_t)(
+            const __attribute__((address_space(3))) uint8_t*)(dst + 1024 * li);
+        uint32_t saved;
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "global_load_lds_dwordx4 %2, off\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved) : "s"(m0), "v"(src + o_) : "memory");
+      }
     }
   };
-  auto stage = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < kLoadsPerThread; ++i) {
-      const int key = tid / 16 + (kThreads / 16) * i;
-      *reinterpret_cast<uint4*>(klds[buf] + key * kKRow + 16 * chunk) = kreg[i];
-      *reinterpret_cast<uint4*>(vlds[buf] + key * kVRow + 16 * chunk) = vreg[i];
-    }
+  auto load_k = [&](int j, int buf) {
+    load_block(kbase, klds[buf], koff, kKPerWave, kKLoads, j, j == nkb - 1);
+  };
+  auto load_v = [&](int j, int buf) {
+    load_block(vbase, vlds[buf], voff, kVPerWave, kVLoads, j, j == nkb - 1);
   };
 
-  const int vrd = (4 * g4 + (r >> 2)) * kVRow + 8 * (r & 3);
-  // One staged key block against this wave's tiles.  On the diagonal block
-  // (the last) keys past a row's position are masked and 16-key tiles that
-  // start past the wave's last position are skipped; every other block is
-  // entirely visible to every row.
-  auto attend = [&](const uint8_t* kb, const uint8_t* vb, int64_t key0, auto diag_tag) {
+  // S^T of the block staged in klds[buf] against every query tile of this
+  // wave (on the diagonal block only the 16-key tiles that some row attends).
+  auto scores = [&](int buf, int ktn, auto diag_tag, f32x4 (&c)[TPW][4]) {
     constexpr bool kDiag = decltype(diag_tag)::value;
-    const int ktn = kDiag ? (int)((pt + 15 - key0) >> 4) + 1 : 4;  // wave-uniform, 1..4
-    // S^T for the attended 16-key tiles of the block, every query tile.
-    f32x4 c[TPW][4];
+    const uint8_t* kb = klds[buf];
 #pragma unroll
     for (int u = 0; u < TPW; ++u)
 #pragma unroll
@@ -215,26 +251,87 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
         for (int u = 0; u < TPW; ++u) c[u][kt] = mfma32(kf, qf[u][s], c[u][kt]);
       }
     }
-    uint4 pa[TPW][2];
-#pragma unroll
-    for (int u = 0; u < TPW; ++u) {
-      // Lane: query pt + r, keys key0 + 16 kt + 4 g4 + i (raw dot products).
-      bool live[4][4];
-      float bm = kNegInf;
+  };
+
+  uint4 pa[TPW][2];
+  // Online softmax of one block's scores: the bf16 probabilities go to pa.
+  // The common case - no row maximum grew past its reference by more than
+  // kLazy - is straight-line code (so the scheduler can interleave it with
+  // the next block's score products); the rare raise of a reference
+  // recomputes that tile's probabilities afterwards, with the same results
+  // as deciding first.
+  auto softmax = [&](f32x4 (&c)[TPW][4], int64_t key0, auto diag_tag, auto hint_tag) {
+    constexpr bool kDiag = decltype(diag_tag)::value;
+    constexpr bool HINT = decltype(hint_tag)::value;
+    float bm[TPW], ps[TPW];
+    auto probabilities = [&](int u) {
+      const float nm = -mq[u];
+      float p[4][4];
+      ps[u] = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          live[kt][i] = !kDiag || key0 + 16 * kt + 4 * g4 + i <= pt + r;
-          bm = fmaxf(bm, live[kt][i] ? c[u][kt][i] : kNegInf);
+          const bool live = !kDiag || key0 + 16 * kt + 4 * g4 + i <= pt + r;
+          p[kt][i] = live ? exp2_hw(fmaf(c[u][kt][i], a.scale_log2, nm)) : 0.0f;
+          ps[u] += p[kt][i];
         }
-      bm = fmaxf(bm, __shfl_xor(bm, 16));
-      bm = fmaxf(bm, __shfl_xor(bm, 32));
-      bm *= a.scale_log2;  // the row's scaled maximum (rounding is monotonic)
-      if (__builtin_amdgcn_ballot_w64(bm > mq[u] + kLazy) != 0) {  // wave-uniform
-        // Raise the offsets to the block maxima; O row 4 g4 + i belongs to
-        // query 4 g4 + i, whose factor lane 4 g4 + i holds.
-        const float mn = fmaxf(mq[u], bm);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        pa[u][ks] = make_uint4(pack2(p[2 * ks][0], p[2 * ks][1]), pack2(p[2 * ks][2], p[2 * ks][3]),
+                               pack2(p[2 * ks + 1][0], p[2 * ks + 1][1]),
+                               pack2(p[2 * ks + 1][2], p[2 * ks + 1][3]));
+    };
+    bool grow = false;
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      float v[16];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool live = !kDiag || key0 + 16 * kt + 4 * g4 + i <= pt + r;
+          v[4 * kt + i] = live ? c[u][kt][i] : kNegInf;
+        }
+      // maximum of the 16 values as a tree of three-input maxima
+      float m = fmaxf(fmaxf(v[0], v[1]), v[2]);
+      m = fmaxf(fmaxf(m, v[3]), v[4]);
+      m = fmaxf(fmaxf(m, v[5]), v[6]);
+      m = fmaxf(fmaxf(m, v[7]), v[8]);
+      m = fmaxf(fmaxf(m, v[9]), v[10]);
+      m = fmaxf(fmaxf(m, v[11]), v[12]);
+      m = fmaxf(fmaxf(m, v[13]), v[14]);
+      m = fmaxf(m, v[15]);
+      {  // the other three lanes of query r: r + 16, r + 32, r + 48
+        const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m),
+                                                          false, false);
+        m = fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+        const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m),
+                                                          false, false);
+        m = fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+      }
+      bm[u] = m * a.scale_log2;  // the row's scaled maximum (rounding is monotonic)
+      grow |= bm[u] > mq[u] + kLazy;
+      probabilities(u);
+    }
+    if constexpr (HINT) {  // beside the next block's scores: interleave
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the key tile's reads
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one product
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // five VALU
+        }
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform, rare
+#pragma unroll
+      for (int u = 0; u < TPW; ++u) {
+        if (__builtin_amdgcn_ballot_w64(bm[u] > mq[u] + kLazy) == 0) continue;
+        // Raise the references to the block maxima; O row 4 g4 + i belongs
+        // to query 4 g4 + i, whose factor lane 4 g4 + i holds.
+        const float mn = fmaxf(mq[u], bm[u]);
         const float corr = exp2_hw(mq[u] - mn);
         lq[u] *= corr;
         mq[u] = mn;
@@ -245,25 +342,17 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
         for (int db = 0; db < 8; ++db)
 #pragma unroll
           for (int i = 0; i < 4; ++i) o[u][db][i] *= cr[i];
+        probabilities(u);
       }
-      const float nm = -mq[u];
-      float p[4][4], ps = 0.0f;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[kt][i] = live[kt][i] ? exp2_hw(fmaf(c[u][kt][i], a.scale_log2, nm)) : 0.0f;
-          ps += p[kt][i];
-        }
-      lq[u] += ps;
-      // The probabilities, rounded to bf16, as the A operand of the two k steps.
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        pa[u][ks] = make_uint4(pack2(p[2 * ks][0], p[2 * ks][1]), pack2(p[2 * ks][2], p[2 * ks][3]),
-                               pack2(p[2 * ks + 1][0], p[2 * ks + 1][1]),
-                               pack2(p[2 * ks + 1][2], p[2 * ks + 1][3]));
     }
-    const int ksn = ktn > 2 ? 2 : 1;  // 32-key steps with an attended tile
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) lq[u] += ps[u];
+  };
+
+  const int vrd = (4 * g4 + (r >> 2)) * kVRow + 8 * (r & 3);
+  auto pv = [&](int buf, int ksn, auto diag_tag) {
+    constexpr bool kDiag = decltype(diag_tag)::value;
+    const uint8_t* vb = vlds[buf];
 #pragma unroll
     for (int db = 0; db < 8; ++db)
 #pragma unroll
@@ -278,19 +367,50 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
       }
   };
 
-  fetch(0);
-  stage(0);
+  // Pipeline: block j + 1's scores (matrix cores) are issued beside block
+  // j's softmax (VALU), then block j's P V.  K blocks run one ahead of V:
+  // during block j the loads of K j + 2 (into K j's buffer) and V j + 1 (into
+  // V j - 1's) fly; one barrier per block.
+  const int dtn = (int)((pt + 15 - (int64_t)(nkb - 1) * kKB) >> 4) + 1;  // diagonal tiles, 1..4
+  const int dks = dtn > 2 ? 2 : 1;
+  f32x4 cc[TPW][4], cn[TPW][4];
+  load_k(0, 0);
+  if (nkb > 1) load_k(1, 1);
+  load_v(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) (every counter)
   __syncthreads();
-  for (int j = 0; j + 1 < nkb; ++j) {
-    // Block j is in buffer j % 2; block j + 1's loads fly during its
-    // arithmetic and land in the other buffer, last read during block j - 1
-    // (before the previous barrier).
-    fetch(j + 1);
-    attend(klds[j & 1], vlds[j & 1], (int64_t)j * kKB, std::false_type{});
-    stage((j + 1) & 1);
+  if (nkb == 1) {
+    scores(0, dtn, std::true_type{}, cc);
+    softmax(cc, 0, std::true_type{}, std::false_type{});
+    pv(0, dks, std::true_type{});
+  } else {
+    scores(0, 4, std::false_type{}, cc);
+    __syncthreads();  // every wave has read K 0: its buffer takes K 2
+    int j = 0;
+    for (; j + 2 < nkb; ++j) {  // block j + 1 is not the diagonal one
+      load_k(j + 2, j & 1);
+      load_v(j + 1, (j + 1) & 1);
+      scores((j + 1) & 1, 4, std::false_type{}, cn);
+      softmax(cc, (int64_t)j * kKB, std::false_type{}, std::true_type{});
+      pv(j & 1, 2, std::false_type{});
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < TPW; ++u)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) cc[u][kt] = cn[u][kt];
+    }
+    // j = nkb - 2: the next block is the diagonal one
+    load_v(j + 1, (j + 1) & 1);
+    scores((j + 1) & 1, dtn, std::true_type{}, cn);
+    softmax(cc, (int64_t)j * kKB, std::false_type{}, std::false_type{});
+    pv(j & 1, 2, std::false_type{});
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    ++j;
+    softmax(cn, (int64_t)j * kKB, std::true_type{}, std::false_type{});
+    pv(j & 1, dks, std::true_type{});
   }
-  attend(klds[(nkb - 1) & 1], vlds[(nkb - 1) & 1], (int64_t)(nkb - 1) * kKB, std::true_type{});
 
   // O / l in bf16, through LDS (this wave's 16 x 128 tile, one tile at a
   // time) so that every lane stores 16 contiguous bytes of one output row.
