@@ -54,7 +54,7 @@ from starter_amd.kernels.prefill import prefill_qkv  # noqa: E402
 from starter_amd.kernels.qk_norm_rope import qk_norm_rope  # noqa: E402
 from starter_amd.kernels.rmsnorm import rms_norm  # noqa: E402
 from starter_amd.kernels.rotary import default_inv_freq, rope_tables  # noqa: E402
-from starter_amd.kernels import row_gemv, skinny_gemm  # noqa: E402
+from starter_amd.kernels import lm_head as _lm_head, row_gemv, skinny_gemm  # noqa: E402
 from starter_amd.kernels.small_query_attention import SmallQueryAttention  # noqa: E402
 
 METRIC = ("achieved HBM GB/s (% of MI355X peak) + µs/call per fused kernel, decode & prefill")
@@ -766,7 +766,8 @@ def profile_run(device, launches: int) -> None:
     """Eager launches for counter collection: a calibration copy of known size
     (CALIBRATION_BYTES read + written by torch's copy kernel), then each
     prefill kernel ``launches`` times on rotating buffer sets, then each decode
-    projection at batch 1, 16 and 64 ``launches`` times on rotating weights."""
+    projection and the LM head at batch 1, 16 and 64 ``launches`` times on
+    rotating weights."""
     src = torch.empty(CALIBRATION_BYTES // 2, dtype=BF16, device=device).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -797,6 +798,17 @@ def profile_run(device, launches: int) -> None:
             order.append(f"{name}_m{m}")
         del weights
         torch.cuda.empty_cache()
+    # The LM head with the greedy choice over the Qwen3-4B vocabulary at the
+    # same batches (projection kernel, then the candidate reduction).
+    heads = [normal((V, H), 0.0, 0.02, g) for _ in range(sets_for(bf16_bytes(V * H)))]
+    for m in (1, 16, 64):
+        x = normal((m, H), g=g)
+        for i in range(launches):
+            _lm_head.lm_head_argmax(x, heads[i % len(heads)])
+        torch.cuda.synchronize()
+        order.append(f"lm_head_m{m}")
+    del heads
+    torch.cuda.empty_cache()
     print(json.dumps({"profile": list(KERNELS), "projections": order, "launches": launches,
                       "calibration_bytes": CALIBRATION_BYTES}), flush=True)
 
