@@ -767,7 +767,7 @@ def profile_run(device, launches: int) -> None:
     (CALIBRATION_BYTES read + written by torch's copy kernel), then each
     prefill kernel ``launches`` times on rotating buffer sets, then each decode
     projection and the LM head at batch 1, 16 and 64 ``launches`` times on
-    rotating weights."""
+    rotating weights, then the prefill attention at 4 x 2048."""
     src = torch.empty(CALIBRATION_BYTES // 2, dtype=BF16, device=device).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -809,6 +809,17 @@ def profile_run(device, launches: int) -> None:
         order.append(f"lm_head_m{m}")
     del heads
     torch.cuda.empty_cache()
+    # The causal prefill attention at 4 x 2048 (the first of its bench cases).
+    from starter_amd.kernels.prefill import prefill_attention
+    batch, length = PREFILL_ATTENTION_CASES[0]
+    q = normal((batch, length, NQ, D), g=g)
+    keys = normal((batch, NK, length + 32, D), g=g)
+    values = normal((batch, NK, length + 32, D), g=g)
+    for _ in range(launches):
+        prefill_attention(q, keys, values, length, D ** -0.5)
+    torch.cuda.synchronize()
+    order.append(f"prefill_attention_b{batch}_t{length}")
+    del q, keys, values
     print(json.dumps({"profile": list(KERNELS), "projections": order, "launches": launches,
                       "calibration_bytes": CALIBRATION_BYTES}), flush=True)
 
