@@ -22,14 +22,17 @@
 // the cache straight into LDS (global_load_lds_dwordx4), K one block ahead
 // of V, so no registers hold them in flight.
 //
-// Pipeline (per wave): block j + 1's score products run on the matrix cores
-// while the VALU does block j's softmax (one scheduling region, interleaved
-// one product to five VALU instructions), then block j's P V.  The softmax
-// VALU work (an exp2, an FMA, a sum, a maximum and half a conversion per
-// score) costs about as many SIMD cycles as the products, so the two only
-// reach the matrix-core bound together; measured (counters, 4 x 2048): the
-// matrix cores 32% busy and the VALU 41% before, with little of the two
-// overlapping.
+// Schedules.  A matrix-core product and VALU work issued by the same wave
+// overlap only about two VALU instructions per product, while VALU work of
+// the SIMD's other wave overlaps the products almost fully (timing probes on
+// gfx950), and the softmax (an exp2, an FMA, a sum and half a conversion per
+// score) is about as much VALU work as the block's products.  So the 8-wave
+// form ping-pongs: waves 0-3 and 4-7 (one of each per SIMD) run the same
+// steps, the second set one step behind; in step M j a wave issues block j -
+// 1's P V and block j's scores (the LDS reads kept 6-8 ahead of the
+// products), in step V j the softmax of block j, and a barrier ends every
+// step.  The 4-wave form (two workgroups per CU, one wave per SIMD each)
+// issues block j + 1's scores beside block j's softmax, then block j's P V.
 //
 // Both products are on the matrix cores (v_mfma_f32_16x16x32_bf16):
 // * Scores, transposed: S^T = K Q^T for a 16-key tile is a chain of four
@@ -44,10 +47,13 @@
 //   address, so lane 4q + t addressing dims 16 db + 4t of key 4 (l / 16) + q
 //   yields keys 4 (l / 16) + 0..3 of dim 16 db + l % 16.  Eight dim tiles of
 //   16 cover the head; lane l accumulates O[query 4 (l / 16) + i][16 db + l % 16].
-// Each lane keeps the running maximum and denominator of its own query
-// (l % 16) over its own keys; the accumulators of query row r are rescaled
-// with the factor of the lanes that own query r (fetched by shuffles) when
-// some row maximum grew past its reference by more than kLazy.  K rows in LDS are 272 bytes (the score
+// Each query row keeps a reference maximum (log2 units, the same on the
+// row's four lanes) and each lane its part of the denominator; probabilities
+// are taken against the reference directly, and the reference is raised -
+// the accumulators rescaled by the factor of the lanes that own each row,
+// fetched by shuffles - only when a lane's sum of its 16 probabilities of a
+// block exceeds 2^kLazy, which any probability above 2^kLazy (and the first
+// block, against a -inf reference) forces.  K rows in LDS are 272 bytes (the score
 // reads, 16 keys at one column per 16-lane group, fall on distinct banks),
 // V rows 288 bytes (the transposing reads, 4 keys x 4 column groups per
 // 16-lane group, on distinct banks).  Keys at or past `length` are never
@@ -73,9 +79,11 @@ constexpr int kORow = 272;              // LDS bytes per row of the output stagi
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kLog2e = 1.4426950408889634f;
 // A row's exponent offset (its reference maximum, log2 units) is raised only
-// when a block's row maximum exceeds it by more than this, so unnormalised
-// probabilities stay below 2^8 and the accumulators are rarely rescaled.
+// when a lane's 16 probabilities of a block sum past 2^kLazy, so
+// unnormalised probabilities stay below 2^8 and the accumulators are rarely
+// rescaled.
 constexpr float kLazy = 8.0f;
+constexpr float kLazyBound = 256.0f;  // 2^kLazy
 
 struct PrefillArgs {
   const uint16_t* q;   // [B, T, Hq, 128]
@@ -255,27 +263,31 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
 
   uint4 pa[TPW][2];
   // Online softmax of one block's scores: the bf16 probabilities go to pa.
-  // The common case - no row maximum grew past its reference by more than
-  // kLazy - is straight-line code (so the scheduler can interleave it with
-  // the next block's score products); the rare raise of a reference
-  // recomputes that tile's probabilities afterwards, with the same results
-  // as deciding first.
+  // The probabilities are taken against the row's reference maximum mq
+  // directly; the reference is raised (and the accumulators rescaled) only
+  // when some lane's sum of its 16 probabilities exceeds 2^kLazy, which any
+  // probability above 2^kLazy (a row maximum more than kLazy above the
+  // reference, or the first block's -inf reference) forces.  The common case
+  // is therefore straight-line code without a row maximum; the rare raise
+  // computes the block's row maxima and recomputes that tile.
   auto softmax = [&](f32x4 (&c)[TPW][4], int64_t key0, auto diag_tag, auto hint_tag) {
     constexpr bool kDiag = decltype(diag_tag)::value;
     constexpr bool HINT = decltype(hint_tag)::value;
-    float bm[TPW], ps[TPW];
+    float ps[TPW];
     auto probabilities = [&](int u) {
       const float nm = -mq[u];
       float p[4][4];
-      ps[u] = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const bool live = !kDiag || key0 + 16 * kt + 4 * g4 + i <= pt + r;
           p[kt][i] = live ? exp2_hw(fmaf(c[u][kt][i], a.scale_log2, nm)) : 0.0f;
-          ps[u] += p[kt][i];
         }
+      float s4[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) s4[kt] = (p[kt][0] + p[kt][1]) + (p[kt][2] + p[kt][3]);
+      ps[u] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         pa[u][ks] = make_uint4(pack2(p[2 * ks][0], p[2 * ks][1]), pack2(p[2 * ks][2], p[2 * ks][3]),
@@ -285,34 +297,8 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
     bool grow = false;
 #pragma unroll
     for (int u = 0; u < TPW; ++u) {
-      float v[16];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const bool live = !kDiag || key0 + 16 * kt + 4 * g4 + i <= pt + r;
-          v[4 * kt + i] = live ? c[u][kt][i] : kNegInf;
-        }
-      // maximum of the 16 values as a tree of three-input maxima
-      float m = fmaxf(fmaxf(v[0], v[1]), v[2]);
-      m = fmaxf(fmaxf(m, v[3]), v[4]);
-      m = fmaxf(fmaxf(m, v[5]), v[6]);
-      m = fmaxf(fmaxf(m, v[7]), v[8]);
-      m = fmaxf(fmaxf(m, v[9]), v[10]);
-      m = fmaxf(fmaxf(m, v[11]), v[12]);
-      m = fmaxf(fmaxf(m, v[13]), v[14]);
-      m = fmaxf(m, v[15]);
-      {  // the other three lanes of query r: r + 16, r + 32, r + 48
-        const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m),
-                                                          false, false);
-        m = fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
-        const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m),
-                                                          false, false);
-        m = fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
-      }
-      bm[u] = m * a.scale_log2;  // the row's scaled maximum (rounding is monotonic)
-      grow |= bm[u] > mq[u] + kLazy;
       probabilities(u);
+      grow |= !(ps[u] <= kLazyBound);  // also a NaN or infinite sum
     }
     if constexpr (HINT) {  // beside the next block's scores: interleave
 #pragma unroll
@@ -321,17 +307,37 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one product
-          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // five VALU
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
         }
       }
     }
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform, rare
 #pragma unroll
       for (int u = 0; u < TPW; ++u) {
-        if (__builtin_amdgcn_ballot_w64(bm[u] > mq[u] + kLazy) == 0) continue;
-        // Raise the references to the block maxima; O row 4 g4 + i belongs
-        // to query 4 g4 + i, whose factor lane 4 g4 + i holds.
-        const float mn = fmaxf(mq[u], bm[u]);
+        if (__builtin_amdgcn_ballot_w64(!(ps[u] <= kLazyBound)) == 0) continue;
+        float v[16];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool live = !kDiag || key0 + 16 * kt + 4 * g4 + i <= pt + r;
+            v[4 * kt + i] = live ? c[u][kt][i] : kNegInf;
+          }
+        float m = v[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) m = fmaxf(m, v[i]);
+        {  // the other three lanes of query r: r + 16, r + 32, r + 48
+          const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m),
+                                                            false, false);
+          m = fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+          const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m),
+                                                            false, false);
+          m = fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+        }
+        // Raise the references to the block maxima (a row whose maximum did
+        // not grow keeps its reference: factor 1); O row 4 g4 + i belongs to
+        // query 4 g4 + i, whose factor lane 4 g4 + i holds.
+        const float mn = fmaxf(mq[u], m * a.scale_log2);
         const float corr = exp2_hw(mq[u] - mn);
         lq[u] *= corr;
         mq[u] = mn;
@@ -367,54 +373,123 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
       }
   };
 
-  // Pipeline: block j + 1's scores (matrix cores) are issued beside block
-  // j's softmax (VALU), then block j's P V.  K blocks run one ahead of V:
-  // during block j the loads of K j + 2 (into K j's buffer) and V j + 1 (into
-  // V j - 1's) fly; one barrier per block.
   const int dtn = (int)((pt + 15 - (int64_t)(nkb - 1) * kKB) >> 4) + 1;  // diagonal tiles, 1..4
   const int dks = dtn > 2 ? 2 : 1;
-  f32x4 cc[TPW][4], cn[TPW][4];
-  load_k(0, 0);
-  if (nkb > 1) load_k(1, 1);
-  load_v(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) (every counter)
-  __syncthreads();
-  if (nkb == 1) {
-    scores(0, dtn, std::true_type{}, cc);
-    softmax(cc, 0, std::true_type{}, std::false_type{});
-    pv(0, dks, std::true_type{});
+  if constexpr (W == 8) {
+    // Ping-pong between the two waves of each SIMD: waves 0-3 and 4-7 run
+    // the same steps, the second set one step behind, so that while one wave
+    // of a SIMD issues matrix-core products (step M j: block j - 1's P V,
+    // then block j's scores) the other runs the VALU softmax of its block
+    // (step V j), and the matrix core is fed from two instruction streams.
+    // A barrier ends every step.  Loads of K j + 1 and V j are issued in
+    // global step 2 j (by every wave) and waited for by the end of step
+    // 2 j + 1; K j and V j - 1 are read in steps 2 j and 2 j + 1.
+    const bool late = wave >= 4;
+    f32x4 cc[TPW][4];
+    auto bar = [] {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto vmwait = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+    auto issue = [&](int jk, int jv) {
+      if (jk < nkb) load_k(jk, jk & 1);
+      if (jv < nkb) load_v(jv, jv & 1);
+    };
+    auto block = [&](int j, auto diag_tag) {
+      constexpr bool kDiag = decltype(diag_tag)::value;
+      if (!late) issue(j + 1, j);
+      if (j > 0) {
+        pv((j - 1) & 1, 2, std::false_type{});
+        scores(j & 1, kDiag ? dtn : 4, diag_tag, cc);
+        if constexpr (!kDiag) {
+          // Keep LDS reads in flight ahead of the products: 8 reads first,
+          // then P V's products one read each, then the scores' products
+          // (two per K fragment) one read per two.
+          __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+          for (int i = 0; i < 24; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        }
+      } else {
+        scores(j & 1, kDiag ? dtn : 4, diag_tag, cc);
+      }
+      if (late) vmwait();
+      bar();
+      if (late) issue(j + 2, j + 1);
+      softmax(cc, (int64_t)j * kKB, diag_tag, std::false_type{});
+      if (!late) vmwait();
+      bar();
+    };
+    load_k(0, 0);
+    vmwait();
+    bar();
+    if (late) {
+      issue(1, 0);
+      bar();
+    }
+    for (int j = 0; j + 1 < nkb; ++j) block(j, std::false_type{});
+    block(nkb - 1, std::true_type{});
+    pv((nkb - 1) & 1, dks, std::true_type{});
+    if (!late) bar();  // the same barrier count for both sets
+    // The output staging below uses the K buffers: the last K reads were in
+    // step 2 nkb - 1, and the second set's last step reads only V.
   } else {
-    scores(0, 4, std::false_type{}, cc);
-    __syncthreads();  // every wave has read K 0: its buffer takes K 2
-    int j = 0;
-    for (; j + 2 < nkb; ++j) {  // block j + 1 is not the diagonal one
-      load_k(j + 2, j & 1);
+    // Pipeline: block j + 1's scores (matrix cores) are issued beside block
+    // j's softmax (VALU), then block j's P V.  K blocks run one ahead of V:
+    // during block j the loads of K j + 2 (into K j's buffer) and V j + 1 (into
+    // V j - 1's) fly; one barrier per block.
+    f32x4 cc[TPW][4], cn[TPW][4];
+    load_k(0, 0);
+    if (nkb > 1) load_k(1, 1);
+    load_v(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) (every counter)
+    __syncthreads();
+    if (nkb == 1) {
+      scores(0, dtn, std::true_type{}, cc);
+      softmax(cc, 0, std::true_type{}, std::false_type{});
+      pv(0, dks, std::true_type{});
+    } else {
+      scores(0, 4, std::false_type{}, cc);
+      __syncthreads();  // every wave has read K 0: its buffer takes K 2
+      int j = 0;
+      for (; j + 2 < nkb; ++j) {  // block j + 1 is not the diagonal one
+        load_k(j + 2, j & 1);
+        load_v(j + 1, (j + 1) & 1);
+        scores((j + 1) & 1, 4, std::false_type{}, cn);
+        softmax(cc, (int64_t)j * kKB, std::false_type{}, std::true_type{});
+        pv(j & 1, 2, std::false_type{});
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < TPW; ++u)
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) cc[u][kt] = cn[u][kt];
+      }
+      // j = nkb - 2: the next block is the diagonal one
       load_v(j + 1, (j + 1) & 1);
-      scores((j + 1) & 1, 4, std::false_type{}, cn);
-      softmax(cc, (int64_t)j * kKB, std::false_type{}, std::true_type{});
+      scores((j + 1) & 1, dtn, std::true_type{}, cn);
+      softmax(cc, (int64_t)j * kKB, std::false_type{}, std::false_type{});
       pv(j & 1, 2, std::false_type{});
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-#pragma unroll
-      for (int u = 0; u < TPW; ++u)
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) cc[u][kt] = cn[u][kt];
+      ++j;
+      softmax(cn, (int64_t)j * kKB, std::true_type{}, std::false_type{});
+      pv(j & 1, dks, std::true_type{});
     }
-    // j = nkb - 2: the next block is the diagonal one
-    load_v(j + 1, (j + 1) & 1);
-    scores((j + 1) & 1, dtn, std::true_type{}, cn);
-    softmax(cc, (int64_t)j * kKB, std::false_type{}, std::false_type{});
-    pv(j & 1, 2, std::false_type{});
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    ++j;
-    softmax(cn, (int64_t)j * kKB, std::true_type{}, std::false_type{});
-    pv(j & 1, dks, std::true_type{});
+    __syncthreads();  // every wave is done with the K/V blocks
   }
 
   // O / l in bf16, through LDS (this wave's 16 x 128 tile, one tile at a
   // time) so that every lane stores 16 contiguous bytes of one output row.
-  __syncthreads();  // every wave is done with the K/V blocks
   uint8_t* ot = reinterpret_cast<uint8_t*>(klds) + wave * 16 * kORow;  // both K buffers
 #pragma unroll
   for (int u = 0; u < TPW; ++u) {
