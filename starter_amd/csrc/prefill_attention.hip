@@ -39,21 +39,23 @@
 //   MFMAs (A = 16 keys x 32 dims from LDS, lane l reading key l % 16, dims
 //   8 (l / 16) + 32 s; B = the tile's 16 query rows, kept in registers),
 //   leaving lane l with S[query l % 16][keys 4 (l / 16) + i].
-// * P V: two 16-key tiles form one 32-wide k step.  Lane l's eight A values
-//   are its own probabilities: keys 4 (l / 16) + i of the first tile and of
-//   the second, in that k-slot order; the B operand must list V in the same
-//   order, which two ds_read_b64_tr_b16 per k step give: lane i of each
-//   16-lane group receives element i % 4 of the 8 bytes lanes 4q + i / 4
-//   address, so lane 4q + t addressing dims 16 db + 4t of key 4 (l / 16) + q
-//   yields keys 4 (l / 16) + 0..3 of dim 16 db + l % 16.  Eight dim tiles of
-//   16 cover the head; lane l accumulates O[query 4 (l / 16) + i][16 db + l % 16].
+// * O^T = V^T P^T: two 16-key tiles form one 32-wide k step.  Lane l's
+//   eight B values are its own probabilities: keys 4 (l / 16) + i of the
+//   first tile and of the second, in that k-slot order; the A operand must
+//   list V in the same order, which two ds_read_b64_tr_b16 per k step give:
+//   lane i of each 16-lane group receives element i % 4 of the 8 bytes lanes
+//   4q + i / 4 address, so lane 4q + t addressing dims 16 db + 4t of key
+//   4 (l / 16) + q yields keys 4 (l / 16) + 0..3 of dim 16 db + l % 16.
+//   Eight dim tiles of 16 cover the head; lane l accumulates dims
+//   16 db + 4 (l / 16) + i of its own query l % 16, so its rescale factor and
+//   denominator are its own and its output is 8 contiguous bytes per db.
 // Each query row keeps a reference maximum (log2 units, the same on the
-// row's four lanes) and each lane its part of the denominator; probabilities
-// are taken against the reference directly, and the reference is raised -
-// the accumulators rescaled by the factor of the lanes that own each row,
-// fetched by shuffles - only when a lane's sum of its 16 probabilities of a
-// block exceeds 2^kLazy, which any probability above 2^kLazy (and the first
-// block, against a -inf reference) forces.  K rows in LDS are 272 bytes (the score
+// row's four lanes) and each lane its part of the denominator.  The first
+// block sets the references to its row maxima; later blocks take their
+// probabilities against the reference directly, and the reference is
+// raised (the accumulators rescaled) only when a lane's sum of its 16
+// probabilities of a block exceeds 2^kLazy, which any probability above
+// 2^kLazy forces.  K rows in LDS are 272 bytes (the score
 // reads, 16 keys at one column per 16-lane group, fall on distinct banks),
 // V rows 288 bytes (the transposing reads, 4 keys x 4 column groups per
 // 16-lane group, on distinct banks).  Keys at or past `length` are never
@@ -263,16 +265,18 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
 
   uint4 pa[TPW][2];
   // Online softmax of one block's scores: the bf16 probabilities go to pa.
-  // The probabilities are taken against the row's reference maximum mq
-  // directly; the reference is raised (and the accumulators rescaled) only
-  // when some lane's sum of its 16 probabilities exceeds 2^kLazy, which any
-  // probability above 2^kLazy (a row maximum more than kLazy above the
-  // reference, or the first block's -inf reference) forces.  The common case
-  // is therefore straight-line code without a row maximum; the rare raise
-  // computes the block's row maxima and recomputes that tile.
-  auto softmax = [&](f32x4 (&c)[TPW][4], int64_t key0, auto diag_tag, auto hint_tag) {
+  // The first block sets each row's reference maximum mq to its row maximum;
+  // later blocks take the probabilities against mq directly and raise it
+  // (rescaling the accumulators) only when some lane's sum of its 16
+  // probabilities exceeds 2^kLazy, which any probability above 2^kLazy (a
+  // row maximum more than kLazy above the reference) forces.  The common
+  // case is therefore straight-line code without a row maximum; the rare
+  // raise computes the block's row maxima and recomputes that tile.
+  auto softmax = [&](f32x4 (&c)[TPW][4], int64_t key0, auto diag_tag, auto hint_tag,
+                     auto first_tag) {
     constexpr bool kDiag = decltype(diag_tag)::value;
     constexpr bool HINT = decltype(hint_tag)::value;
+    constexpr bool kFirst = decltype(first_tag)::value;
     float ps[TPW];
     auto probabilities = [&](int u) {
       const float nm = -mq[u];
@@ -294,6 +298,32 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
                                pack2(p[2 * ks + 1][0], p[2 * ks + 1][1]),
                                pack2(p[2 * ks + 1][2], p[2 * ks + 1][3]));
     };
+    // The row maximum of this block's live scores, over the four lanes of
+    // each query.
+    auto row_max = [&](int u) {
+      float m = kNegInf;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool live = !kDiag || key0 + 16 * kt + 4 * g4 + i <= pt + r;
+          m = fmaxf(m, live ? c[u][kt][i] : kNegInf);
+        }
+      const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m),
+                                                        false, false);
+      m = fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+      const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m),
+                                                        false, false);
+      return fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+    };
+    if constexpr (kFirst) {  // the first block: the references start at its row maxima
+#pragma unroll
+      for (int u = 0; u < TPW; ++u) {
+        mq[u] = row_max(u) * a.scale_log2;
+        probabilities(u);
+        lq[u] = ps[u];
+      }
+    } else {
     bool grow = false;
 #pragma unroll
     for (int u = 0; u < TPW; ++u) {
@@ -315,44 +345,24 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
 #pragma unroll
       for (int u = 0; u < TPW; ++u) {
         if (__builtin_amdgcn_ballot_w64(!(ps[u] <= kLazyBound)) == 0) continue;
-        float v[16];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool live = !kDiag || key0 + 16 * kt + 4 * g4 + i <= pt + r;
-            v[4 * kt + i] = live ? c[u][kt][i] : kNegInf;
-          }
-        float m = v[0];
-#pragma unroll
-        for (int i = 1; i < 16; ++i) m = fmaxf(m, v[i]);
-        {  // the other three lanes of query r: r + 16, r + 32, r + 48
-          const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m),
-                                                            false, false);
-          m = fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
-          const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m),
-                                                            false, false);
-          m = fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
-        }
+        const float m = row_max(u);
         // Raise the references to the block maxima (a row whose maximum did
-        // not grow keeps its reference: factor 1); O row 4 g4 + i belongs to
-        // query 4 g4 + i, whose factor lane 4 g4 + i holds.
+        // not grow keeps its reference: factor 1); this lane's accumulators
+        // all belong to its own query.
         const float mn = fmaxf(mq[u], m * a.scale_log2);
         const float corr = exp2_hw(mq[u] - mn);
         lq[u] *= corr;
         mq[u] = mn;
-        float cr[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cr[i] = __shfl(corr, 4 * g4 + i);
 #pragma unroll
         for (int db = 0; db < 8; ++db)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) o[u][db][i] *= cr[i];
+          for (int i = 0; i < 4; ++i) o[u][db][i] *= corr;
         probabilities(u);
       }
     }
 #pragma unroll
     for (int u = 0; u < TPW; ++u) lq[u] += ps[u];
+    }
   };
 
   const int vrd = (4 * g4 + (r >> 2)) * kVRow + 8 * (r & 3);
@@ -369,7 +379,7 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
         const uint4 vt = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
                                     __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
 #pragma unroll
-        for (int u = 0; u < TPW; ++u) o[u][db] = mfma32(pa[u][ks], vt, o[u][db]);
+        for (int u = 0; u < TPW; ++u) o[u][db] = mfma32(vt, pa[u][ks], o[u][db]);
       }
   };
 
@@ -396,7 +406,7 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
       if (jk < nkb) load_k(jk, jk & 1);
       if (jv < nkb) load_v(jv, jv & 1);
     };
-    auto block = [&](int j, auto diag_tag) {
+    auto block = [&](int j, auto diag_tag, auto first_tag) {
       constexpr bool kDiag = decltype(diag_tag)::value;
       if (!late) issue(j + 1, j);
       if (j > 0) {
@@ -425,7 +435,7 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
       if (late) vmwait();
       bar();
       if (late) issue(j + 2, j + 1);
-      softmax(cc, (int64_t)j * kKB, diag_tag, std::false_type{});
+      softmax(cc, (int64_t)j * kKB, diag_tag, std::false_type{}, first_tag);
       if (!late) vmwait();
       bar();
     };
@@ -436,12 +446,15 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
       issue(1, 0);
       bar();
     }
-    for (int j = 0; j + 1 < nkb; ++j) block(j, std::false_type{});
-    block(nkb - 1, std::true_type{});
+    if (nkb == 1) {
+      block(0, std::true_type{}, std::true_type{});
+    } else {
+      block(0, std::false_type{}, std::true_type{});
+      for (int j = 1; j + 1 < nkb; ++j) block(j, std::false_type{}, std::false_type{});
+      block(nkb - 1, std::true_type{}, std::false_type{});
+    }
     pv((nkb - 1) & 1, dks, std::true_type{});
     if (!late) bar();  // the same barrier count for both sets
-    // The output staging below uses the K buffers: the last K reads were in
-    // step 2 nkb - 1, and the second set's last step reads only V.
   } else {
     // Pipeline: block j + 1's scores (matrix cores) are issued beside block
     // j's softmax (VALU), then block j's P V.  K blocks run one ahead of V:
@@ -455,7 +468,7 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
     __syncthreads();
     if (nkb == 1) {
       scores(0, dtn, std::true_type{}, cc);
-      softmax(cc, 0, std::true_type{}, std::false_type{});
+      softmax(cc, 0, std::true_type{}, std::false_type{}, std::true_type{});
       pv(0, dks, std::true_type{});
     } else {
       scores(0, 4, std::false_type{}, cc);
@@ -465,7 +478,8 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
         load_k(j + 2, j & 1);
         load_v(j + 1, (j + 1) & 1);
         scores((j + 1) & 1, 4, std::false_type{}, cn);
-        softmax(cc, (int64_t)j * kKB, std::false_type{}, std::true_type{});
+        if (j == 0) softmax(cc, 0, std::false_type{}, std::false_type{}, std::true_type{});
+        else softmax(cc, (int64_t)j * kKB, std::false_type{}, std::true_type{}, std::false_type{});
         pv(j & 1, 2, std::false_type{});
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -477,36 +491,32 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
       // j = nkb - 2: the next block is the diagonal one
       load_v(j + 1, (j + 1) & 1);
       scores((j + 1) & 1, dtn, std::true_type{}, cn);
-      softmax(cc, (int64_t)j * kKB, std::false_type{}, std::false_type{});
+      if (j == 0) softmax(cc, 0, std::false_type{}, std::false_type{}, std::true_type{});
+      else softmax(cc, (int64_t)j * kKB, std::false_type{}, std::false_type{}, std::false_type{});
       pv(j & 1, 2, std::false_type{});
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       ++j;
-      softmax(cn, (int64_t)j * kKB, std::true_type{}, std::false_type{});
+      softmax(cn, (int64_t)j * kKB, std::true_type{}, std::false_type{}, std::false_type{});
       pv(j & 1, dks, std::true_type{});
     }
-    __syncthreads();  // every wave is done with the K/V blocks
   }
 
-  // O / l in bf16, through LDS (this wave's 16 x 128 tile, one tile at a
-  // time) so that every lane stores 16 contiguous bytes of one output row.
+  // O / l in bf16 through LDS (this wave's 16 x 128 tile; lane l writes the
+  // 8 bytes of dims 16 db + 4 g4 .. + 3 of its own query), read back so that
+  // every lane stores 16 contiguous bytes of one output row.
+  if constexpr (W != 8) __syncthreads();  // every wave is done with the K blocks
   uint8_t* ot = reinterpret_cast<uint8_t*>(klds) + wave * 16 * kORow;  // both K buffers
 #pragma unroll
   for (int u = 0; u < TPW; ++u) {
     float lt = lq[u] + __shfl_xor(lq[u], 16);
-    lt += __shfl_xor(lt, 32);  // lanes of query r: its denominator
-    float inv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float den = __shfl(lt, 4 * g4 + i);
-      inv[i] = 1.0f / den;
-    }
+    lt += __shfl_xor(lt, 32);  // the four lanes of query r: its denominator
+    const float inv = 1.0f / lt;
 #pragma unroll
     for (int db = 0; db < 8; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<uint16_t*>(ot + (4 * g4 + i) * kORow + 2 * (16 * db + r)) =
-            to_bf16(o[u][db][i] * inv[i]);
+      *reinterpret_cast<uint2*>(ot + r * kORow + 2 * (16 * db + 4 * g4)) =
+          make_uint2(pack2(o[u][db][0] * inv, o[u][db][1] * inv),
+                     pack2(o[u][db][2] * inv, o[u][db][3] * inv));
     wave_lds_fence();
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
