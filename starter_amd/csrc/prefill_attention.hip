@@ -107,8 +107,11 @@ struct PrefillArgs {
 // G * QB query rows, so its K/V traffic from L2 per flop falls as that grows:
 // at G = 4, 8 waves of 64 positions (256 rows) need half the block loads of
 // two 4-wave workgroups of 32 (the same two waves per SIMD).
-// WIDE (8 waves) is taken when the grid still has two workgroups per CU;
-// smaller prompts keep the 4-wave form's twice as many workgroups.
+// WIDE (8 waves, the ping-pong schedule) is taken when the grid has at least
+// one workgroup per CU: measured against the 4-wave form, 16% faster at
+// 1 x 2048 and 11% at 4 x 512 (256 workgroups), about even at 128 (1 x 1024
+// +4%, 2 x 512 -5%), so smaller prompts keep the 4-wave form's twice as
+// many workgroups.
 template <int G, bool WIDE> struct Split;
 template <bool WIDE> struct Split<1, WIDE> { static constexpr int QB = 64, TPW = 1, W = 4; };
 template <bool WIDE> struct Split<2, WIDE> { static constexpr int QB = 64, TPW = 2, W = 4; };
@@ -116,7 +119,7 @@ template <> struct Split<4, false> { static constexpr int QB = 32, TPW = 2, W = 
 template <> struct Split<4, true> { static constexpr int QB = 64, TPW = 2, W = 8; };
 template <> struct Split<8, false> { static constexpr int QB = 16, TPW = 2, W = 4; };
 template <> struct Split<8, true> { static constexpr int QB = 32, TPW = 2, W = 8; };
-constexpr int64_t kWideWorkgroups = 2 * kCUs;
+constexpr int64_t kWideWorkgroups = kCUs;
 
 __device__ __forceinline__ f32x4 mfma32(const uint4& a, const uint4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),

@@ -99,9 +99,10 @@ def test_monotone_scores(climb):
 @pytest.mark.parametrize("b,t,hq,hk,seq,kvh", [
     (4, 2048, 16, 4, 3, 1),   # G = 4: 512 workgroups of 64 positions (8 waves)
     (4, 1024, 32, 4, 1, 3),   # G = 8: 512 workgroups of 32 positions (8 waves)
+    (1, 2048, 32, 8, 0, 5),   # G = 4: 256 workgroups, one per CU (8 waves)
 ])
 def test_wide_workgroups_match_oracle_slices(b, t, hq, hk, seq, kvh):
-    """Grids of >= 512 workgroups take the 8-wave form; one (sequence, KV
+    """Grids of >= 256 workgroups take the 8-wave form; one (sequence, KV
     head) slice of its output against the float64 oracle of that slice."""
     q, k, v = operands(b, t, hq, hk, t + 8, 880 + t + hq)
     out = prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV), t, SCALE)
