@@ -56,6 +56,7 @@ from starter_amd.kernels.rmsnorm import rms_norm  # noqa: E402
 from starter_amd.kernels.rotary import default_inv_freq, rope_tables  # noqa: E402
 from starter_amd.kernels import lm_head as _lm_head, row_gemv, skinny_gemm  # noqa: E402
 from starter_amd.kernels.small_query_attention import SmallQueryAttention  # noqa: E402
+from starter_amd.engine import KEY_ALIGN  # noqa: E402
 
 METRIC = ("achieved HBM GB/s (% of MI355X peak) + µs/call per fused kernel, decode & prefill")
 PEAK_GBPS = 8000.0          # MI355X HBM3E, AMD specification
@@ -378,7 +379,7 @@ def decode_attention_bench(device, replays: int = 20, calls: int = GRAPH_CALLS) 
         caches = [(normal((batch, NK, cap, D), g=g), normal((batch, NK, cap, D), g=g)) for _ in range(sets)]
         q = normal((batch, NQ, 1, D), g=g)
         used = torch.full((batch * NK,), cap, dtype=torch.int32, device=device)
-        plan = SmallQueryAttention(batch, NQ, NK, cap, device)
+        plan = SmallQueryAttention(batch, NQ, NK, cap, device, key_align=KEY_ALIGN)
         ours = lambda i: plan.run(q, *caches[i % sets], used, D ** -0.5)
         base = lambda i: torch.nn.functional.scaled_dot_product_attention(
             q, *caches[i % sets], scale=D ** -0.5, enable_gqa=True)

@@ -356,6 +356,20 @@ int qf_attention_partition(int64_t virtual_heads, int64_t capacity, int32_t comp
                            int32_t* splits, int64_t* span);
 
 /*
+ * The plan qf_attention_partition aims for (at most one workgroup per CU,
+ * at most 32 segments, at least one 64-key tile each) with the segment
+ * lengths balanced to `align` (16, 32 or 64) keys instead of whole 64-key
+ * tiles, so the aimed-for count is kept where 64-key rounding drops a
+ * segment (4 x 2081 keys: 8 x 272 instead of 7 x 320): span a multiple of
+ * align, (splits - 1) * span < capacity <= splits * span.  No counterpart in
+ * the reference, whose partition_keys contract fixes 64-key tiles; the
+ * Engine's decode step uses align 16 (qf_decode_attention accepts any span
+ * that is a multiple of 16).
+ */
+int qf_attention_partition_aligned(int64_t virtual_heads, int64_t capacity, int32_t compute_units,
+                                   int32_t align, int32_t* splits, int64_t* span);
+
+/*
  * Decode attention, one query token per sequence, grouped-query heads:
  *   q bf16 [batch, q_heads, 1, 128]; k, v bf16 [batch, kv_heads, capacity, 128]
  *   (all contiguous); used int32 [batch * kv_heads] on the device: keys

@@ -976,23 +976,48 @@ int launch_attn(const AttnArgs& args, int64_t vheads, hipStream_t s) {
 
 using namespace qf;
 
-extern "C" int qf_attention_partition(int64_t virtual_heads, int64_t capacity,
-                                      int32_t compute_units, int32_t* splits, int64_t* span) {
-  if (virtual_heads < 1 || capacity < 1 || compute_units < 1 || !splits || !span) return QF_E_ARG;
-  // At most one workgroup per compute unit (measured with the matrix-core
-  // kernel at batch x keys from 1 x 545 to 64 x 1024 against every split
-  // count: a CU that runs two segments finishes last, so 1.25 per CU - the
-  // earlier plan - cost 4-17% at batch 4 x 545, 16 and 32; fewer segments
-  // lengthen each workgroup's chain), at least one 64-key tile per segment,
-  // at most 32 segments; segments are whole 64-key tiles.
+namespace {
+// Segments per (sequence, KV head): at most one workgroup per compute unit
+// (measured with the matrix-core kernel at batch x keys from 1 x 545 to
+// 64 x 1024 against every split count: a CU that runs two segments finishes
+// last, so 1.25 per CU - the earlier plan - cost 4-17% at batch 4 x 545, 16
+// and 32; fewer segments lengthen each workgroup's chain), at least one
+// 64-key tile per segment, at most 32 segments.
+int64_t segment_count(int64_t virtual_heads, int64_t capacity, int32_t compute_units) {
   const int64_t tiles = (capacity + 63) / 64;
   const int64_t desired = (int64_t)compute_units / virtual_heads;
   int64_t s = desired < 1 ? 1 : desired;
   if (s > tiles) s = tiles;
   if (s > kMaxSplits) s = kMaxSplits;
-  const int64_t per = (tiles + s - 1) / s;
-  *splits = (int32_t)((tiles + per - 1) / per);
-  *span = per * 64;
+  return s;
+}
+
+// s segments of whole `unit`-key multiples covering capacity, as balanced as
+// that granularity allows.
+void segment_plan(int64_t capacity, int64_t s, int64_t unit, int32_t* splits, int64_t* span) {
+  const int64_t units = (capacity + unit - 1) / unit;
+  const int64_t per = (units + s - 1) / s;
+  *splits = (int32_t)((units + per - 1) / per);
+  *span = per * unit;
+}
+}  // namespace
+
+extern "C" int qf_attention_partition(int64_t virtual_heads, int64_t capacity,
+                                      int32_t compute_units, int32_t* splits, int64_t* span) {
+  if (virtual_heads < 1 || capacity < 1 || compute_units < 1 || !splits || !span) return QF_E_ARG;
+  segment_plan(capacity, segment_count(virtual_heads, capacity, compute_units), 64, splits, span);
+  return QF_OK;
+}
+
+extern "C" int qf_attention_partition_aligned(int64_t virtual_heads, int64_t capacity,
+                                              int32_t compute_units, int32_t align,
+                                              int32_t* splits, int64_t* span) {
+  if (virtual_heads < 1 || capacity < 1 || compute_units < 1 || !splits || !span) return QF_E_ARG;
+  if (align != 16 && align != 32 && align != 64) return QF_E_ARG;
+  // The same segment count with lengths balanced to `align` keys (at 4 x
+  // 2081 keys: 8 x 272 instead of 7 x 320, one workgroup per CU instead of
+  // 224 of 256).
+  segment_plan(capacity, segment_count(virtual_heads, capacity, compute_units), align, splits, span);
   return QF_OK;
 }
 

@@ -134,6 +134,12 @@ def check_rotary(model) -> None:
 #: batches lose: 2,806 against 2,389 us/step at 4 x 2048, 3,364 against 2,480
 #: at 8 x 1024, 4,468 against 2,669 at 16 x 512, same tokens).
 MERGED_O_BATCH = 1
+#: Key-segment granularity of the decode attention's plan: the segment count
+#: of partition_keys with lengths balanced to 16 keys (4 x 2081 keys: 8 x 272
+#: instead of 7 x 320, 10.6 against 11.3 us; 16 x 641: 2 x 336 instead of
+#: 2 x 384, 11.8 against 12.2 us; batch 1 unchanged).
+KEY_ALIGN = 16
+
 #: Largest batch whose decode step folds the add + norm launches into the
 #: projections around them where their shapes allow (measured on Qwen3-4B:
 #: batch 1 1,989 against 2,121 us/step with the down/qkv fold alone and
@@ -210,7 +216,8 @@ class _State:
         self.keys = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in engine.layers]
         self.values = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in engine.layers]
         self.cos, self.sin = rope_tables(engine.inv_freq, capacity, device=dev)
-        self.attention = SmallQueryAttention(batch, engine.q_heads, engine.kv_heads, capacity, dev)
+        self.attention = SmallQueryAttention(batch, engine.q_heads, engine.kv_heads, capacity, dev,
+                                             key_align=KEY_ALIGN)
         # o_proj merges the attention's key segments itself (one launch fewer
         # per layer) up to MERGED_O_BATCH sequences.
         self.merged_o = (batch <= MERGED_O_BATCH and self.attention.splits > 1

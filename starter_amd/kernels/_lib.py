@@ -59,6 +59,7 @@ SIGNATURES = {
     "qf_linear_silu_mul_normed_tiled": ([_vp, _vp, _vp, _f32, _i64, _i64, _vp, _i64, _vp, _vp],
                                         _i32),
     "qf_attention_partition": ([_i64, _i64, _i32, _vp, _vp], _i32),
+    "qf_attention_partition_aligned": ([_i64, _i64, _i32, _i32, _vp, _vp], _i32),
     "qf_decode_attention": ([_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _f32, _i32, _i64, _vp, _vp,
                              _vp, _vp], _i32),
     "qf_decode_attention_qkv": ([_vp, _i32, _vp, _vp, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp,

@@ -23,7 +23,7 @@ def declared() -> set[str]:
 def test_header_and_binding_agree():
     names = declared()
     assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
-    assert len(names) == 32
+    assert len(names) == 33
 
 
 def test_library_exports_every_symbol():
@@ -126,6 +126,8 @@ def test_host_side_argument_errors_launch_nothing():
     split, span = ctypes.c_int32(), ctypes.c_int64()
     assert lib.qf_attention_partition(0, 64, 256, ctypes.byref(split), ctypes.byref(span)) == -1
     assert lib.qf_attention_partition(8, 545, 256, None, ctypes.byref(span)) == -1
+    assert lib.qf_attention_partition_aligned(8, 545, 256, 8, ctypes.byref(split), ctypes.byref(span)) == -1
+    assert lib.qf_attention_partition_aligned(8, 545, 256, 16, None, ctypes.byref(span)) == -1
     assert lib.qf_decode_attention(bogus, bogus, bogus, bogus, 1, 34, 2, 64, 0.1, 1, 64, None, None,
                                    bogus, None) == -2
     assert lib.qf_decode_attention(bogus, bogus, bogus, bogus, 1, 8, 3, 64, 0.1, 1, 64, None, None,

@@ -94,8 +94,8 @@ def test_every_split_plan_matches_the_oracle():
     q, k, v = normal((b, hq, 1, 128), g=g), normal((b, hk, cap, 128), g=g), normal((b, hk, cap, 128), g=g)
     used = torch.tensor([1100, 1, 64, 65, 700, 1099, 0, 513] * 2, dtype=torch.int32)
     qd, kd, vd, ud = q.to(DEV), poison(k, used).to(DEV), poison(v, used).to(DEV), used.to(DEV)
-    for splits in (1, 2, 5, 18):
-        span = -(-((cap + 63) // 64) // splits) * 64
+    for splits, align in ((1, 64), (2, 64), (5, 64), (18, 64), (5, 16), (8, 16), (13, 32), (32, 48)):
+        span = -(-(-(-cap // align)) // splits) * align   # 16-key multiples are enough
         splits = -(-cap // span)
         part = torch.empty((b * hk, splits, hq // hk, 128), dtype=torch.float32, device=DEV)
         stats = torch.empty((b * hk, splits, 2, hq // hk), dtype=torch.float32, device=DEV)

@@ -402,6 +402,26 @@ def test_attention_partition_contract():
             partition_keys(*args)
 
 
+def test_aligned_attention_partition_contract():
+    """The finer plan: the same coverage rules at 16/32/64-key granularity,
+    the segment count partition_keys aims for (one per CU, <= 32, >= one
+    64-key tile each), and the 64-key plan itself at align 64."""
+    from starter_amd.kernels.small_query_attention import partition_keys, partition_keys_aligned
+    for heads in (1, 8, 24, 32, 128, 512, 4096):
+        for capacity in (1, 15, 16, 17, 63, 64, 65, 544, 545, 641, 2080, 2081, 8193, 262144):
+            for units in (1, 80, 114, 256):
+                aim = max(1, min(units // heads, -(-capacity // 64), 32))
+                for align in (16, 32, 64):
+                    splits, span = partition_keys_aligned(heads, capacity, units, align)
+                    assert 1 <= splits <= aim and span % align == 0
+                    assert (splits - 1) * span < capacity <= splits * span
+                assert partition_keys_aligned(heads, capacity, units, 64) == partition_keys(heads, capacity, units)
+    assert partition_keys_aligned(32, 2081, 256, 16) == (8, 272)
+    for args in ((0, 1, 1, 16), (1, 0, 1, 16), (1, 1, 0, 16), (1, 1, 1, 8), (1, 1, 1, 128)):
+        with pytest.raises(ValueError):
+            partition_keys_aligned(*args)
+
+
 def test_attention_context_validation_and_marshalling():
     from starter_amd.kernels import small_query_attention as sqa
     props = mock.Mock(multi_processor_count=256)
