@@ -41,6 +41,7 @@ import torch
 
 from .kernels import _lib
 from .kernels.rotary import default_inv_freq, rope_tables
+from .engine import KEY_ALIGN
 from .kernels.small_query_attention import SmallQueryAttention
 
 NQ, NK, D = 32, 8, 128
@@ -92,7 +93,7 @@ def measure(batch: int, keys: int, qkv_splits: int, calls: int = 24, replays: in
     def normal(shape, mean=0.0, std=1.0):
         return (torch.randn(shape, generator=g, device=device) * std + mean).to(torch.bfloat16)
 
-    plan = SmallQueryAttention(batch, NQ, NK, keys, device)
+    plan = SmallQueryAttention(batch, NQ, NK, keys, device, key_align=KEY_ALIGN)  # the Engine's plan
     vheads, splits = batch * NK, plan.splits
     width = (NQ + 2 * NK) * D
     kv_bytes = 2 * batch * NK * keys * D * 2
@@ -226,7 +227,7 @@ def table(results) -> str:
         line(f"attention phase {p}: → {name}", name)
     line("  of phase 6: the slowest wave's key loop ends after wave 0's by", BARRIER_NAMES[0])
     line("  of phase 6: barrier passed after the slowest wave's loop", BARRIER_NAMES[1])
-    line("  of phase 6: wave 0's merge of the four waves", BARRIER_NAMES[2])
+    line("  of phase 6: the merge of the four waves", BARRIER_NAMES[2])
     line("spread of the four waves' first-block times", "first_block_spread")
     line("hand-off: last attention store → first merge start", "handoff")
     line("merge: start → its loads landed", "merge_load")
