@@ -21,6 +21,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kWave = 64;
 constexpr int kBlock = 256;  // 4 waves per workgroup everywhere
 constexpr int kCUs = 256;    // MI355X compute units (sizes launch plans)
+constexpr int kXCDs = 8;     // MI355X dies; workgroup i of a grid runs on XCD i % 8
 
 // ---- bf16 <-> f32 -----------------------------------------------------------
 

@@ -8,7 +8,9 @@ tolerance against float64 (rtol 0.02, atol 0.004; tests/test_small_query_
 attention.py in the reference), and an RMS error below 1% of the RMS output.
 Shapes cover 1, 2, 4 and 8 query heads per KV head, prompts that end inside a
 query block and inside a key block, one token, and the Qwen3-4B head layout;
-cache slots past the prompt hold NaN and must never reach the output.  Known
+cache slots past the prompt hold NaN and must never reach the output.  The
+8-wave form's grouped work orders must write every block of an output that
+starts as NaN.  Known
 answers: zero queries give the running mean of V exactly; inputs stay
 untouched; a captured graph replays with new contents.  Scores that climb
 across key blocks (every block raises the row maxima by more than the lazy
@@ -112,6 +114,34 @@ def test_wide_workgroups_match_oracle_slices(b, t, hq, hk, seq, kvh):
     check(out[seq:seq + 1, :, heads].cpu(), q[seq:seq + 1, :, heads].contiguous(),
           k[seq:seq + 1, kvh:kvh + 1].contiguous(), v[seq:seq + 1, kvh:kvh + 1].contiguous(), t,
           f"b{b} t{t} hq{hq} hk{hk} slice ({seq}, {kvh})")
+
+
+@pytest.mark.parametrize("b,t", [
+    (16, 512),   # 4 (sequence, KV head) pairs per XCD and group, 4 groups
+    (8, 256),    # 4 per group, 2 groups
+    (64, 128),   # 8 per group (two query blocks each), 8 groups
+    (4, 2048),   # 4 pairs per XCD: the plain order
+])
+def test_grouped_work_orders_write_every_block(b, t):
+    """The 8-wave form walks the pairs of each XCD a group at a time; every
+    (query block, pair) must be computed exactly once.  The whole output,
+    written into NaN, against torch's flash kernel (Qwen3-4B heads)."""
+    from starter_amd.kernels import _lib
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    g = torch.Generator(device=DEV).manual_seed(b + t)
+    hq, hk, cap = 32, 8, t + 16
+    q = torch.randn(b, t, hq, 128, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(b, hk, cap, 128, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(b, hk, cap, 128, generator=g, device=DEV).to(torch.bfloat16)
+    out = torch.full_like(q, float("nan"))
+    _lib.call("qf_prefill_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), b, t, hq, hk, cap,
+              SCALE, out.data_ptr(), _lib.stream(q.device))
+    with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            q.transpose(1, 2), k[:, :, :t], v[:, :, :t], is_causal=True, scale=SCALE,
+            enable_gqa=True).transpose(1, 2)
+    assert not torch.isnan(out).any()
+    torch.testing.assert_close(out.float(), ref.float(), rtol=0.02, atol=0.004)
 
 
 def test_zero_queries_give_the_running_mean():
