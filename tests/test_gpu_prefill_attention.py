@@ -10,9 +10,8 @@ Shapes cover 1, 2, 4 and 8 query heads per KV head, prompts that end inside a
 query block and inside a key block, one token, and the Qwen3-4B head layout;
 cache slots past the prompt hold NaN and must never reach the output.  The
 8-wave form's grouped work orders must write every block of an output that
-starts as NaN.  Known
-answers: zero queries give the running mean of V exactly; inputs stay
-untouched; a captured graph replays with new contents.  Scores that climb
+starts as NaN.  Known answers: zero queries give the running mean of V
+exactly; inputs stay untouched; a captured graph replays with new contents.  Scores that climb
 across key blocks (every block raises the row maxima by more than the lazy
 rescale threshold) and that fall (no block after the first raises them), and
 negative and zero scales (Q enters negated, exact in bf16), cover the
@@ -116,20 +115,22 @@ def test_wide_workgroups_match_oracle_slices(b, t, hq, hk, seq, kvh):
           f"b{b} t{t} hq{hq} hk{hk} slice ({seq}, {kvh})")
 
 
-@pytest.mark.parametrize("b,t", [
-    (16, 512),   # 4 (sequence, KV head) pairs per XCD and group, 4 groups
-    (8, 256),    # 4 per group, 2 groups
-    (64, 128),   # 8 per group (two query blocks each), 8 groups
-    (4, 2048),   # 4 pairs per XCD: the plain order
+@pytest.mark.parametrize("b,t,hq,hk", [
+    (16, 512, 32, 8),   # 4 (sequence, KV head) pairs per XCD and group, 4 groups
+    (8, 256, 32, 8),    # 4 per group, 2 groups
+    (64, 128, 32, 8),   # 8 per group (two query blocks each), 8 groups
+    (6, 1024, 32, 8),   # 6 pairs per XCD: groups of 3
+    (4, 2048, 32, 8),   # 4 pairs per XCD: the plain order
+    (5, 1664, 8, 2),    # 10 pairs, not a multiple of the XCD count: the plain order
 ])
-def test_grouped_work_orders_write_every_block(b, t):
+def test_grouped_work_orders_write_every_block(b, t, hq, hk):
     """The 8-wave form walks the pairs of each XCD a group at a time; every
     (query block, pair) must be computed exactly once.  The whole output,
-    written into NaN, against torch's flash kernel (Qwen3-4B heads)."""
+    written into NaN, against torch's flash kernel."""
     from starter_amd.kernels import _lib
     from torch.nn.attention import SDPBackend, sdpa_kernel
     g = torch.Generator(device=DEV).manual_seed(b + t)
-    hq, hk, cap = 32, 8, t + 16
+    cap = t + 16
     q = torch.randn(b, t, hq, 128, generator=g, device=DEV).to(torch.bfloat16)
     k = torch.randn(b, hk, cap, 128, generator=g, device=DEV).to(torch.bfloat16)
     v = torch.randn(b, hk, cap, 128, generator=g, device=DEV).to(torch.bfloat16)
