@@ -146,7 +146,8 @@ __global__ __launch_bounds__(kBlock) void rms_vec_kernel(RmsArgs a) {
 // unconditional (a lane past the row end re-reads the row's last vector and
 // contributes zero), so the compiler has no branch to sink them under.
 template <int VPL, int R, int MODE, bool FULL, bool NT>
-__device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int lane) {
+__device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int64_t rstride,
+                                            int lane) {
   constexpr bool ADD = MODE == 1;
   const int last = a.nvec - 1;
   const uint4* wv4 = reinterpret_cast<const uint4*>(a.w);
@@ -158,7 +159,7 @@ __device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int 
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const uint4* xin = reinterpret_cast<const uint4*>(row_base<ADD>(a, row0 + r));
+    const uint4* xin = reinterpret_cast<const uint4*>(row_base<ADD>(a, row0 + r * rstride));
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
       const int v = lane + k * kWave;
@@ -166,14 +167,14 @@ __device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int 
       xv[r][k] = load16<NT>(xin + vv);
       if constexpr (ADD) {
         const uint4* bin = reinterpret_cast<const uint4*>(
-            static_cast<const uint16_t*>(a.branch) + (row0 + r) * a.cols);
+            static_cast<const uint16_t*>(a.branch) + (row0 + r * rstride) * a.cols);
         bv[r][k] = load16<NT>(bin + vv);
       }
     }
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t row = row0 + r;
+    const int64_t row = row0 + r * rstride;
     float t[VPL][8];
     double ss = 0.0;
 #pragma unroll
@@ -214,18 +215,30 @@ __device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int 
   }
 }
 
-// One wave per RPW consecutive rows; the grid's last wave, whose rows may run
-// past a.rows, takes its rows one at a time.
-template <int VPL, int RPW, int MODE, bool FULL, bool NT = true>
+// A wave takes RPW rows, run by run (ILV false: rows RPW w .. RPW w + RPW - 1)
+// or interleaved: the grid's waves go in rounds of kCUs * 4 waves (one 4-wave
+// workgroup per CU), and wave i of a round of n waves takes rows base + i,
+// base + i + n, .., base + i + (RPW - 1) n, so each round streams one
+// contiguous front of rows.  A wave whose last row would run past a.rows
+// takes its rows one at a time.
+template <int VPL, int RPW, int MODE, bool FULL, bool NT = true, bool ILV = false>
 __global__ __launch_bounds__(kBlock) void rms_stream_kernel(RmsArgs a) {
   const int lane = threadIdx.x % kWave;
-  const int64_t row0 = __builtin_amdgcn_readfirstlane(
-      ((int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave) * RPW);
-  if (row0 + RPW <= a.rows) {
-    stream_rows<VPL, RPW, MODE, FULL, NT>(a, row0, lane);
+  const int64_t w = __builtin_amdgcn_readfirstlane(
+      (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave);
+  int64_t row0 = w * RPW, step = 1;
+  if constexpr (ILV) {
+    constexpr int64_t kRound = (int64_t)kCUs * (kBlock / kWave);
+    const int64_t waves = (int64_t)gridDim.x * (kBlock / kWave);
+    const int64_t q = w / kRound;
+    step = waves - q * kRound < kRound ? waves - q * kRound : kRound;
+    row0 = q * kRound * RPW + w % kRound;
+  }
+  if (row0 + (RPW - 1) * step < a.rows) {
+    stream_rows<VPL, RPW, MODE, FULL, NT>(a, row0, step, lane);
   } else {
-    for (int64_t row = row0; row < a.rows; ++row)  // wave-uniform
-      stream_rows<VPL, 1, MODE, FULL, NT>(a, row, lane);
+    for (int64_t row = row0; row < a.rows; row += step)  // wave-uniform
+      stream_rows<VPL, 1, MODE, FULL, NT>(a, row, step, lane);
   }
 }
 
@@ -283,12 +296,21 @@ int launch_rows(const RmsArgs& a, hipStream_t s) {
 // Large calls stream with nontemporal accesses and, for rows of at most five
 // vectors per lane (<= 2560 columns) with a bf16 or no branch, two rows per
 // wave; decode-size calls keep one row per wave and cached accesses.
+// Interleaved rows (ILV) for rows of at most five vectors per lane once the
+// grid fills every CU, measured on the residual add + norm: [8192, 2560]
+// 28.2 -> 27.0 us, [16384, 2560] 62.8 -> 59.3, [32768, 2560] 126.4 -> 120.3,
+// [4096, 2560] 14.2 -> 13.9; wider rows ([8192, 4096]: 45.5 -> 48.1) and
+// grids under one workgroup per CU ([3000, 2560]: 11.2 -> 12.2) keep runs.
 template <int VPL, int RPW, int MODE>
 int launch_stream(const RmsArgs& a, hipStream_t s) {
   constexpr int64_t per_block = kBlock / kWave * RPW;
   const int64_t blocks = (a.rows + per_block - 1) / per_block;
-  hipLaunchKernelGGL((rms_stream_kernel<VPL, RPW, MODE, true>), dim3((unsigned)blocks),
-                     dim3(kBlock), 0, s, a);
+  if (VPL <= 5 && RPW > 1 && blocks >= kCUs)
+    hipLaunchKernelGGL((rms_stream_kernel<VPL, RPW, MODE, true, true, true>), dim3((unsigned)blocks),
+                       dim3(kBlock), 0, s, a);
+  else
+    hipLaunchKernelGGL((rms_stream_kernel<VPL, RPW, MODE, true>), dim3((unsigned)blocks),
+                       dim3(kBlock), 0, s, a);
   return launch_status();
 }
 

@@ -190,15 +190,18 @@ def test_add_rms_norm_config4a_full_size():
 @pytest.mark.parametrize("rows,cols", [
     (1700, 2560),   # 2 rows per wave, partial last wave
     (3000, 2560),   # 4 rows per wave, partial last wave
-    (8195, 2560),   # 8 rows per wave, 3 rows left for the last wave
-    (20000, 2560),  # 8 rows per wave, several workgroups per CU
+    (2047, 2560),   # interleaved rows: 2 per wave, one round, the last row missing
+    (4096, 2560),   # interleaved rows: 4 per wave, one exact round
+    (8195, 2560),   # interleaved rows: 8 per wave, a second round of 4 waves
+    (20000, 2560),  # interleaved rows: 8 per wave, two full rounds and a partial one
     (1100, 4096),   # 8 vectors per lane: at most 4 rows per wave
     (2600, 8192),   # 16 vectors per lane: at most 2 rows per wave
     (2000, 2056),   # rows ending mid-vector-group keep the one-to-two-row kernel
 ])
 def test_add_rms_norm_streaming_row_plans(rows, cols):
-    """Calls of at least 32 MiB stream several rows per wave; every plan and a
-    partial last wave match the oracle bit for bit, for both outputs."""
+    """Calls of at least 32 MiB stream several rows per wave, in runs or
+    interleaved over rounds of one workgroup per CU; every plan and a partial
+    last wave or round match the oracle bit for bit, for both outputs."""
     g = gen(rows + cols)
     x, y = normal((rows, cols), g=g), normal((rows, cols), 0.0, 3.0, g=g)
     w = normal((cols,), 1.0, 0.1, g=g)
