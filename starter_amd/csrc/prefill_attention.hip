@@ -15,8 +15,8 @@
 // and QB consecutive query positions for all G query heads of that KV head,
 // i.e. G QB / 16 tiles of 16 query rows (one head, 16 positions); wave w
 // takes tiles w, w + W, ...  Workgroups run longest first (the last query
-// blocks attend the most keys), in the 8-wave form per group of pairs on
-// each XCD (see work order below).  Keys stream in blocks of 64, staged once per
+// blocks attend the most keys), on grids of at least one workgroup per CU
+// per group of pairs on each XCD (see work order below).  Keys stream in blocks of 64, staged once per
 // workgroup in LDS and shared by every tile, so the K/V bytes a CU pulls from
 // L2 per flop shrink with the workgroup's query rows (the per-CU L2 request
 // rate, not the matrix cores, bounded the 4-wave form).  The blocks go from
@@ -550,14 +550,14 @@ __global__ __launch_bounds__((Split<G, WIDE>::W * kWave)) void prefill_attn_kern
   }
 }
 
-// Pairs per XCD and group of the 8-wave form's work order: at least 4, and
+// Pairs per XCD and group of the wide grids' work order: at least 4, and
 // at least 16 / qblocks, a divisor of the pairs each XCD holds (0 where
 // that is one group, i.e. the plain order, or the pairs do not divide among
 // the XCDs).  Measured on Qwen3-4B heads (8 calls per graph, the same
 // tensors): 16 x 512 61.3 -> 56.7 us, 32 x 256 49.2 -> 44.2, 64 x 128 (8 per
 // group) 42.9 -> 39.8, 8 x 1024 83.1 -> 81.6; 4 x 2048 holds 4 pairs per
-// XCD, its plain order.  The 4-wave form's grids (under one workgroup per
-// CU) measured the same in either order.
+// XCD, its plain order.  Grids under one workgroup per CU measured the
+// same in either order.
 int32_t work_group(int32_t pairs, int32_t qblocks) {
   if (pairs % kXCDs != 0) return 0;
   const int32_t per_xcd = pairs / kXCDs;
