@@ -221,15 +221,17 @@ __device__ __forceinline__ void stream_rows(const RmsArgs& a, int64_t row0, int6
 // base + i + n, .., base + i + (RPW - 1) n, so each round streams one
 // contiguous front of rows.  A wave whose last row would run past a.rows
 // takes its rows one at a time.
-template <int VPL, int RPW, int MODE, bool FULL, bool NT = true, bool ILV = false>
+// WPB: waves per workgroup (4, or 1 for decode sizes).
+template <int VPL, int RPW, int MODE, bool FULL, bool NT = true, bool ILV = false,
+          int WPB = kBlock / kWave>
 __global__ __launch_bounds__(kBlock) void rms_stream_kernel(RmsArgs a) {
   const int lane = threadIdx.x % kWave;
   const int64_t w = __builtin_amdgcn_readfirstlane(
-      (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave);
+      (int64_t)blockIdx.x * WPB + threadIdx.x / kWave);
   int64_t row0 = w * RPW, step = 1;
   if constexpr (ILV) {
-    constexpr int64_t kRound = (int64_t)kCUs * (kBlock / kWave);
-    const int64_t waves = (int64_t)gridDim.x * (kBlock / kWave);
+    constexpr int64_t kRound = (int64_t)kCUs * WPB;
+    const int64_t waves = (int64_t)gridDim.x * WPB;
     const int64_t q = w / kRound;
     step = waves - q * kRound < kRound ? waves - q * kRound : kRound;
     row0 = q * kRound * RPW + w % kRound;
@@ -340,12 +342,14 @@ int launch_vec(const RmsArgs& a, hipStream_t s) {
   const int64_t bytes = a.rows * a.cols * 2 * (MODE == 0 ? 2 : 4);
   if (bytes < kStreamBytes) {
     // Decode sizes: one row per wave, cached accesses; whole-group rows take
-    // the loads-before-stores kernel.
+    // the loads-before-stores kernel with one wave per workgroup, so the rows
+    // spread over as many CUs as there are rows (the 36-call [64, 2560]
+    // add + norm chain: 2.89 -> 2.66 us per call against four waves per
+    // workgroup; [16, 2560] 2.84 -> 2.62).
     if constexpr (LPR == 64 && MODE != 2) {
       if (a.nvec == VPL * kWave) {
-        const int64_t blocks = (a.rows + kBlock / kWave - 1) / (kBlock / kWave);
-        hipLaunchKernelGGL((rms_stream_kernel<VPL, 1, MODE, true, false>), dim3((unsigned)blocks),
-                           dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((rms_stream_kernel<VPL, 1, MODE, true, false, false, 1>),
+                           dim3((unsigned)a.rows), dim3(kWave), 0, s, a);
         return launch_status();
       }
     }
