@@ -32,8 +32,9 @@
 // steps, the second set one step behind; in step M j a wave issues block j -
 // 1's P V and block j's scores (the LDS reads kept 6-8 ahead of the
 // products), in step V j the softmax of block j, and a barrier ends every
-// step.  The 4-wave form (two workgroups per CU, one wave per SIMD each)
-// issues block j + 1's scores beside block j's softmax, then block j's P V.
+// step.  The 4-wave form issues block j + 1's scores beside block j's
+// softmax, then block j's P V; at G = 4 its waves hold one 16-row tile each,
+// which leaves room for two workgroups per CU.
 //
 // Both products are on the matrix cores (v_mfma_f32_16x16x32_bf16):
 // * Scores, transposed: S^T = K Q^T for a 16-key tile is a chain of four
@@ -107,17 +108,24 @@ struct PrefillArgs {
 // one diagonal block), W waves per workgroup and TPW 16-row tiles per wave,
 // G * QB / 16 = W * TPW.  Each staged key block serves all of a workgroup's
 // G * QB query rows, so its K/V traffic from L2 per flop falls as that grows:
-// at G = 4, 8 waves of 64 positions (256 rows) need half the block loads of
-// two 4-wave workgroups of 32 (the same two waves per SIMD).
+// at G = 4, 8 waves of 64 positions (256 rows) need a quarter of the block
+// loads of four 4-wave workgroups of 16.
 // WIDE (8 waves, the ping-pong schedule) is taken when the grid has at least
-// one workgroup per CU: measured against the 4-wave form, 16% faster at
-// 1 x 2048 and 11% at 4 x 512 (256 workgroups), about even at 128 (1 x 1024
-// +4%, 2 x 512 -5%), so smaller prompts keep the 4-wave form's twice as
-// many workgroups.
+// one workgroup per CU (1 x 2048, 4 x 512 and up at Qwen3-4B's heads).
+// Smaller prompts take the 4-wave form, which at G = 4 holds 16 positions
+// per workgroup (one tile per wave, 157 VGPRs: two workgroups per CU; with
+// 32 positions and two tiles per wave it needed 312 registers, one
+// workgroup per CU) - four times the 8-wave form's workgroups, each with a
+// shorter chain per key block.  Measured (Qwen3-4B heads, bit-identical
+// outputs): 1 x 512 18.7 -> 13.4 us, 2 x 512 19.3 -> 15.5, 3 x 512 20.5 ->
+// 18.7, 1 x 1024 32.3 -> 24.4, 1 x 1536 45.7 -> 34.6 against 32 positions;
+// the 8-wave form stays ahead from one workgroup per CU (1 x 2048 53.9
+// against 57.1 us, 4 x 512 21.2 against 21.9) and behind below it (1 x 1024
+// 30.8, 3 x 512 20.5 at 128 and 192 workgroups).
 template <int G, bool WIDE> struct Split;
 template <bool WIDE> struct Split<1, WIDE> { static constexpr int QB = 64, TPW = 1, W = 4; };
 template <bool WIDE> struct Split<2, WIDE> { static constexpr int QB = 64, TPW = 2, W = 4; };
-template <> struct Split<4, false> { static constexpr int QB = 32, TPW = 2, W = 4; };
+template <> struct Split<4, false> { static constexpr int QB = 16, TPW = 1, W = 4; };
 template <> struct Split<4, true> { static constexpr int QB = 64, TPW = 2, W = 8; };
 template <> struct Split<8, false> { static constexpr int QB = 16, TPW = 2, W = 4; };
 template <> struct Split<8, true> { static constexpr int QB = 32, TPW = 2, W = 8; };
