@@ -836,17 +836,17 @@ int dispatch_partials(const SkinnyArgs& a, int splits, hipStream_t s) {
   }
 }
 
-// Gate/up + SiLU: all of K per workgroup.  Up to 8 rows one tile of 8 gate
+// Gate/up + SiLU: all of K per workgroup.  Up to 12 rows one tile of 8 gate
 // over 8 up rows per workgroup (1,216 workgroups for Qwen3-4B: 10% faster at
 // 1-4 rows than a gate and an up tile per wave, whose 608 larger workgroups
-// leave the stream's end unbalanced; same bits); 9..16 rows the tile pair;
-// beyond 16 rows one gate and one up tile per wave, four waves sharing each
-// staged x chunk.
+// leave the stream's end unbalanced, 4% at 9-10 rows, even at 12-14, 1%
+// slower at 16; same bits); 13..16 rows the tile pair; beyond 16 rows one
+// gate and one up tile per wave, four waves sharing each staged x chunk.
 int dispatch_silu(const SkinnyArgs& a, hipStream_t s) {
   switch ((a.m + kTile - 1) / kTile) {
     case 1:
       if (a.m <= 4) return launch<1, 1, 4, 4, kEpiSiluMul, true, kXDirect>(a, 1, s);
-      if (a.m <= 8) return launch<1, 1, 4, 4, kEpiSiluMul, true, kXStaged>(a, 1, s);
+      if (a.m <= 12) return launch<1, 1, 4, 4, kEpiSiluMul, true, kXStaged>(a, 1, s);
       return launch<1, 2, 4, 4, kEpiSiluMul, true, kXStaged>(a, 1, s);
     case 2: return launch_xs<2, 2, 1, 4, kEpiSiluMul>(a, 1, s);
     case 3: return launch_xs<3, 2, 1, 4, kEpiSiluMul>(a, 1, s);

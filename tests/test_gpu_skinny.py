@@ -81,7 +81,7 @@ def test_partials_integer_exact_every_path(m):
         np.testing.assert_array_equal(p.cpu().numpy(), O.linear_partials(bits(x), bits(w), splits))
 
 
-@pytest.mark.parametrize("m", [1, 4, 5, 8, 9, 16, 17, 33, 64])  # 8 | 9: half-tile | tile pairs
+@pytest.mark.parametrize("m", [1, 4, 5, 8, 9, 12, 13, 16, 17, 33, 64])  # 12 | 13: half tile | tile pairs
 @pytest.mark.parametrize("n", [64, 96])  # 96: the last workgroup has waves past N
 def test_silu_mul_integer_exact_every_path(m, n):
     g = gen(80 + m + n)
@@ -102,7 +102,7 @@ def test_partials_qwen_shapes_integer_exact(name, m):
     torch.testing.assert_close(got.cpu(), exact_int_partials(x, w, got.shape[0]), rtol=0, atol=0)
 
 
-@pytest.mark.parametrize("m", [1, 4, 8, 16, 32, 48, 64])
+@pytest.mark.parametrize("m", [1, 4, 8, 12, 13, 16, 32, 48, 64])
 def test_silu_mul_qwen_shape_integer_exact(m):
     n, k = GATE_UP
     g = gen(120 + m)
