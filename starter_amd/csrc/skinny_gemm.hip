@@ -937,8 +937,14 @@ int dispatch_argmax(const SkinnyArgs& a, hipStream_t s) {
         if (a.m <= 4) return launch<1, 1, 4, 4, kEpiArgmax, true, kXDirect>(a, 1, s);
         return launch_xs<1, 1, 1, 4, kEpiArgmax>(a, 1, s);
       }
+      // 5-16 rows share each staged x chunk among the waves: 32 columns per
+      // workgroup (two wave groups of one tile) up to 8 rows, 128 (four
+      // groups of two) beyond, where x's re-reads weigh more (measured on
+      // the Qwen3-4B head against 64 columns: 122.6 -> 119.1 us at 5 rows,
+      // 124.5 -> 122.3 at 8, 129.0 -> 126.0 at 16).
       if (a.m <= 4) return launch<1, 2, 4, 4, kEpiArgmax, true, kXDirect>(a, 1, s);
-      return launch_xs<1, 2, 2, 4, kEpiArgmax>(a, 1, s);
+      if (a.m <= 8) return launch_xs<1, 1, 2, 4, kEpiArgmax>(a, 1, s);
+      return launch_xs<1, 2, 1, 4, kEpiArgmax>(a, 1, s);
     case 2: return two ? launch_xs<2, 2, 1, 4, kEpiArgmax>(a, 1, s) : launch_xs<2, 1, 1, 4, kEpiArgmax>(a, 1, s);
     case 3: return two ? launch_xs<3, 2, 1, 4, kEpiArgmax>(a, 1, s) : launch_xs<3, 1, 1, 4, kEpiArgmax>(a, 1, s);
     default: return two ? launch_xs<4, 2, 1, 4, kEpiArgmax>(a, 1, s) : launch_xs<4, 1, 1, 4, kEpiArgmax>(a, 1, s);

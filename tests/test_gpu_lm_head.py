@@ -25,8 +25,9 @@ from starter_amd.kernels.lm_head import lm_head_argmax  # noqa: E402
 DEV = "cuda"
 
 
-@pytest.mark.parametrize("m", [1, 3, 4, 5, 16, 17, 33, 64])
-@pytest.mark.parametrize("vocab", [4096, 4112])  # 4112: a partly filled last workgroup
+@pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 9, 16, 17, 33, 64])
+# 4112: 16-column tiles only; 4128: a partly filled last 64- or 128-column workgroup
+@pytest.mark.parametrize("vocab", [4096, 4112, 4128])
 def test_integer_logits_and_tied_tokens_exact(m, vocab):
     g = gen(600 + m + vocab)
     x = torch.zeros(m, 256, dtype=torch.bfloat16)
