@@ -10,6 +10,9 @@ at most 2.0 logits, and wherever the native top two differ by more than 0.25
 it must be the native argmax.  Graph replay must equal eager stepping bit for bit,
 and a local safetensors checkpoint must give the same generation.
 
+A generation abandoned by its consumer, or one whose prefill raised, leaves
+the engine usable for the next call.
+
 The contract cases of tests/test_qk_norm_rope.py:201-220 in the reference
 ((3, 7, 5) twice, (1, 1, 3), (2, 13, 1), (2, 13, 0)): exactly ``count``
 lists of ``batch`` ids, each token within 2.0 logits of the native maximum
@@ -176,6 +179,53 @@ def test_graph_replay_equals_eager(engine):
     eager_tokens, eager_logits = run(eager, other, 5)
     assert torch.equal(new_tokens, eager_tokens) and torch.equal(new_logits, eager_logits)
     assert not torch.equal(new_logits, graph_logits)
+
+
+def test_abandoned_generation_keeps_a_usable_state(engine):
+    """A consumer that stops after two of six steps (the generator closed
+    early) leaves the state usable: the next call of the same shape gives the
+    uninterrupted result, on the same buffers, which the captured graphs
+    address (engine/decode.py keeps its buffer addresses across prompts,
+    tests/test_decode.py:91 in the reference)."""
+    prompts = [[11, 12, 13, 14, 15], [21, 22, 23, 24, 25]]
+    full_tokens, full_logits = run(engine, prompts, 6)
+    st = engine.state
+    buffers = (st.prompt, st.tokens, st.position, st.used, st.keys[0], st.values[-1])
+    addresses = [t.data_ptr() for t in buffers]
+    stream = engine.generate(prompts, 6)
+    next(stream)
+    next(stream)
+    stream.close()
+    again_tokens, again_logits = run(engine, prompts, 6)
+    assert engine.state is st
+    assert [t.data_ptr() for t in buffers] == addresses
+    assert torch.equal(again_tokens, full_tokens) and torch.equal(again_logits, full_logits)
+
+
+def test_prefill_error_leaves_the_engine_usable(engine, monkeypatch):
+    """An exception raised inside the prefill (here injected into its first
+    warm-up run on a new shape) reaches the caller, and the next call of that
+    shape captures and generates as if nothing had happened
+    (tests/test_prefill.py:447-466 in the reference)."""
+    prompts = [[31, 32, 33, 34, 35, 36]]
+    real = engine._prefill
+    calls = []
+
+    def failing(st):
+        calls.append(st.key)
+        if len(calls) == 1:
+            raise RuntimeError("injected")
+        return real(st)
+
+    monkeypatch.setattr(engine, "_prefill", failing)
+    with pytest.raises(RuntimeError, match="injected"):
+        list(engine.generate(prompts, 4))
+    assert torch.cuda.current_stream() == torch.cuda.default_stream()
+    tokens, logits = run(engine, prompts, 4)
+    monkeypatch.undo()
+    fresh = Engine(config=Qwen3Config(**TINY), seed=3, keep_logits=True)
+    fresh_tokens, fresh_logits = run(fresh, prompts, 4)
+    assert torch.equal(tokens, fresh_tokens) and torch.equal(logits, fresh_logits)
 
 
 def test_local_checkpoint(engine, tmp_path):
