@@ -482,9 +482,16 @@ class Engine:
 
     # ------------------------------------------------------------ generate
 
-    @torch.inference_mode()
+    @torch.no_grad()
     def generate(self, input_ids: list[list[int]], max_new_tokens: int):
-        """Greedy continuation; yields one list[int] per step, max_new_tokens times."""
+        """Greedy continuation; yields one list[int] per step, max_new_tokens times.
+
+        Runs under ``no_grad`` rather than ``inference_mode``: the first HIP
+        graph captured in a process creates torch's graph-safe RNG state
+        tensors, and captured under inference mode they would be inference
+        tensors, which every later capture outside inference mode (the
+        caller's own graphs) must update in place and cannot while this
+        engine's graphs exist."""
         if max_new_tokens <= 0:
             return
         if not input_ids:

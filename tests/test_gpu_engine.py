@@ -228,6 +228,25 @@ def test_prefill_error_leaves_the_engine_usable(engine, monkeypatch):
     assert torch.equal(tokens, fresh_tokens) and torch.equal(logits, fresh_logits)
 
 
+def test_caller_graphs_capture_after_generation():
+    """After a generation (whose prefill and decode graphs stay alive), a
+    graph the caller captures outside inference mode still captures and
+    replays: the engine's captures leave torch's graph RNG state ordinary
+    tensors."""
+    other = Engine(config=Qwen3Config(**TINY), seed=4)
+    assert len(list(other.generate([[1, 2, 3, 4]], 3))) == 3
+    assert other.state.graph is not None and not torch.is_inference_mode_enabled()
+    x = torch.zeros(4, device="cuda")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        y = x + 1
+    graph.replay()
+    torch.cuda.synchronize()
+    assert y.tolist() == [1.0] * 4
+
+
 def test_local_checkpoint(engine, tmp_path):
     engine.model.save_pretrained(tmp_path, safe_serialization=True)
     loaded = Engine(str(tmp_path), keep_logits=True)
