@@ -45,7 +45,8 @@ def check(out, q, k, v, used):
 
 CASES = ((1, 4, 1, 1), (1, 4, 1, 63), (1, 4, 1, 65), (1, 32, 8, 544), (2, 6, 2, 257),
          (3, 8, 2, 129), (1, 16, 1, 193), (1, 8, 1, 641), (1, 4, 1, 1025), (4, 32, 8, 2080),
-         (16, 32, 8, 640), (1, 1, 1, 65), (1, 8, 1, 300))
+         (16, 32, 8, 640), (1, 1, 1, 65), (1, 8, 1, 300),
+         (1, 32, 8, 16400), (2, 32, 8, 8200))  # long contexts: 32 and 16 segments of 512+ keys
 
 
 @pytest.mark.parametrize("b,hq,hk,cap", CASES)

@@ -61,6 +61,8 @@ def check(got, q, k, v, t, what, scale=SCALE):
     (1, 64, 16, 2, 64),     # G = 8, capacity = length
     (1, 200, 32, 8, 256),   # Qwen3-4B heads, several key blocks
     (2, 129, 32, 8, 130),   # one position past a key block
+    (3, 333, 32, 8, 340),   # 4-wave form over 16-position blocks, 6 key blocks
+    (1, 700, 32, 8, 704),   # ... 11 key blocks, rescales across many blocks
 ])
 def test_matches_oracle(b, t, hq, hk, cap):
     q, k, v = operands(b, t, hq, hk, cap, 800 + t + hq)
