@@ -11,7 +11,7 @@ composed and checked end to end:
 * batch 2: gate/up normalising its input inside the matrix-core tiles, and
   a 2 x 2048 prompt - 4,096 rows, the prefill attention's 8-wave form;
 * batch 3: the folded path with three rows padded to four;
-* batches 4 and 16: the split-K projections with separate add + norm
+* batches 4, 8, 12 and 16: the split-K projections with separate add + norm
   launches;
 * every batch: the LM head over the full 151,936-column vocabulary fused
   with the greedy choice, inside the captured decode graph.
@@ -77,7 +77,8 @@ def run(engine, prompts, steps):
 
 
 @pytest.mark.parametrize("batch,length,steps", [(1, 545, 4), (2, 2048, 3), (3, 600, 3),
-                                                (4, 1100, 3), (16, 641, 3)])
+                                                (4, 1100, 3), (8, 300, 3), (12, 200, 3),
+                                                (16, 641, 3)])
 def test_qwen3_4b_widths_teacher_forced(engines, batch, length, steps):
     engine, native = engines
     g = torch.Generator().manual_seed(4000 + 7 * batch + length)
