@@ -933,16 +933,16 @@ int dispatch_argmax(const SkinnyArgs& a, hipStream_t s) {
   const bool two = a.n % (2 * kTile) == 0;
   switch ((a.m + kTile - 1) / kTile) {
     case 1:
-      if (a.m == 1 || !two) {
-        if (a.m <= 4) return launch<1, 1, 4, 4, kEpiArgmax, true, kXDirect>(a, 1, s);
-        return launch_xs<1, 1, 1, 4, kEpiArgmax>(a, 1, s);
-      }
+      // Up to 4 rows (x as broadcast lines): one 16-column tile per
+      // workgroup, the most workgroups (Qwen3-4B head at 2 and 3 rows: 117.8
+      // -> 114.8 and 118.3 -> 115.7 us against two tiles; even at 4).
+      if (a.m <= 4) return launch<1, 1, 4, 4, kEpiArgmax, true, kXDirect>(a, 1, s);
+      if (!two) return launch_xs<1, 1, 1, 4, kEpiArgmax>(a, 1, s);
       // 5-16 rows share each staged x chunk among the waves: 32 columns per
       // workgroup (two wave groups of one tile) up to 8 rows, 128 (four
       // groups of two) beyond, where x's re-reads weigh more (measured on
       // the Qwen3-4B head against 64 columns: 122.6 -> 119.1 us at 5 rows,
       // 124.5 -> 122.3 at 8, 129.0 -> 126.0 at 16).
-      if (a.m <= 4) return launch<1, 2, 4, 4, kEpiArgmax, true, kXDirect>(a, 1, s);
       if (a.m <= 8) return launch_xs<1, 1, 2, 4, kEpiArgmax>(a, 1, s);
       return launch_xs<1, 2, 1, 4, kEpiArgmax>(a, 1, s);
     case 2: return two ? launch_xs<2, 2, 1, 4, kEpiArgmax>(a, 1, s) : launch_xs<2, 1, 1, 4, kEpiArgmax>(a, 1, s);
